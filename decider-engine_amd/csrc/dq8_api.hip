@@ -1,0 +1,381 @@
+// C ABI of include/dq8.h on top of the HIP kernels in dq8_kernels.hip.
+#include "../../include/dq8.h"
+#include "dq8_internal.h"
+
+#include <new>
+#include <stdint.h>
+#include <string.h>
+
+struct dq8_ctx {
+  int device;
+  // Workspace for padded / freshly quantized activations.  Grows, never shrinks;
+  // only dq8_linear_f32in and K % 64 != 0 inputs use it.
+  void* work = nullptr;
+  size_t work_bytes = 0;
+  uint32_t* flag = nullptr;  // non-finite flag for synchronous checks
+};
+
+struct dq8_weights {
+  dq8::Weights w;
+};
+
+namespace {
+
+using dq8::kGroup;
+
+size_t groups_of(size_t k) { return (k + kGroup - 1) / kGroup; }
+
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = true;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+dq8_status from_hip(hipError_t e) {
+  if (e == hipSuccess) return DQ8_OK;
+  if (e == hipErrorOutOfMemory) return DQ8_ERR_NOMEM;
+  return DQ8_ERR_DEVICE;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+dq8_status ensure_work(dq8_ctx* ctx, size_t bytes) {
+  if (bytes <= ctx->work_bytes) return DQ8_OK;
+  if (ctx->work) {
+    // Earlier work queued on any stream may still read the old buffer.
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return from_hip(e);
+    (void)hipFree(ctx->work);
+    ctx->work = nullptr;
+    ctx->work_bytes = 0;
+  }
+  size_t want = bytes + (bytes >> 2);
+  hipError_t e = hipMalloc(&ctx->work, want);
+  if (e != hipSuccess) return from_hip(e);
+  ctx->work_bytes = want;
+  return DQ8_OK;
+}
+
+dq8_status make_weights(dq8_ctx* ctx, size_t n, size_t k, dq8_weights** out) {
+  if (n == 0 || k == 0 || n > (1u << 30) || k > (1u << 30) || n * k > ((size_t)1 << 40)) return DQ8_ERR_SHAPE;
+  dq8_weights* h = new (std::nothrow) dq8_weights();
+  if (!h) return DQ8_ERR_NOMEM;
+  h->w.device = ctx->device;
+  h->w.n = (int)n;
+  h->w.k = (int)k;
+  h->w.g = (int)groups_of(k);
+  h->w.np = (int)((n + dq8::kColPad - 1) / dq8::kColPad * dq8::kColPad);
+  h->w.values = nullptr;
+  h->w.scales = nullptr;
+  hipError_t e = hipMalloc(&h->w.values, (size_t)h->w.np * h->w.g * kGroup);
+  if (e == hipSuccess) e = hipMalloc(&h->w.scales, (size_t)h->w.np * h->w.g * sizeof(float));
+  if (e != hipSuccess) {
+    (void)hipFree(h->w.values);
+    (void)hipFree(h->w.scales);
+    delete h;
+    return from_hip(e);
+  }
+  *out = h;
+  return DQ8_OK;
+}
+
+// Fill a launch item.  q must already satisfy the kernel's requirements.
+void fill_proj(dq8::Proj& p, const dq8::Weights& w, const int8_t* q, int ldq, const float* xs, size_t m,
+               const float* bias, float* out, int32_t* dots, int layout, int epilogue) {
+  p.q = q;
+  p.xs = xs;
+  p.wt = w.values;
+  p.wst = w.scales;
+  p.bias = bias;
+  p.out = out;
+  p.dots = dots;
+  p.m = (int)m;
+  p.ldq = ldq;
+  p.g = w.g;
+  p.n = w.n;
+  p.np = w.np;
+  p.epilogue = epilogue;
+  p.layout = layout;
+}
+
+// Quantized inputs are usable by the kernels directly when rows are 16-byte
+// aligned and every group is complete; otherwise they are copied, zero-padded
+// to G*64 bytes per row, into the context workspace.
+bool needs_pad(const dq8::Weights& w, const int8_t* q) { return w.k % kGroup != 0 || !aligned(q, 16); }
+size_t pad_bytes(const dq8::Weights& w, size_t m) { return (m * (size_t)w.g * kGroup + 255) / 256 * 256; }
+
+dq8_status check_item_args(const dq8_weights* w, const int8_t* q, const float* scales, size_t m, float* out,
+                           dq8_layout layout, dq8_epilogue epilogue) {
+  if (!w || !q || !scales || !out) return DQ8_ERR_ARG;
+  if (layout != DQ8_ROWS && layout != DQ8_COLUMNS) return DQ8_ERR_ARG;
+  if (epilogue != DQ8_WRITE && epilogue != DQ8_ADD && epilogue != DQ8_SWIGLU) return DQ8_ERR_ARG;
+  if (layout == DQ8_COLUMNS && epilogue != DQ8_WRITE) return DQ8_ERR_ARG;
+  if (m > (1u << 30)) return DQ8_ERR_SHAPE;
+  return DQ8_OK;
+}
+
+// Split items by kernel kind and launch.  Items with m == 0 do nothing (tensor.rs:152-154).
+dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, int32_t* dots, hipStream_t s) {
+  size_t need = 0;
+  for (size_t i = 0; i < count; ++i)
+    if (items[i].m && needs_pad(items[i].w->w, items[i].q)) need += pad_bytes(items[i].w->w, items[i].m);
+  if (need) {
+    dq8_status st = ensure_work(ctx, need);
+    if (st != DQ8_OK) return st;
+  }
+  dq8::Batch batch[2];
+  batch[0].count = batch[1].count = 0;
+  batch[0].total_waves = batch[1].total_waves = 0;
+  size_t offset = 0;
+  for (size_t i = 0; i < count; ++i) {
+    const dq8_linear_item& it = items[i];
+    if (it.m == 0) continue;
+    const dq8::Weights& w = it.w->w;
+    const int kind = it.m <= 32 ? 1 : 0;
+    dq8::Batch& b = batch[kind];
+    if (b.count == dq8::kMaxBatch) {
+      hipError_t e = dq8::launch_linear(b, kind, dots != nullptr, s);
+      if (e != hipSuccess) return from_hip(e);
+      b.count = 0;
+      b.total_waves = 0;
+    }
+    const int8_t* q = it.q;
+    int ldq = w.k;
+    if (needs_pad(w, it.q)) {
+      int8_t* dst = (int8_t*)ctx->work + offset;
+      ldq = w.g * kGroup;
+      hipError_t e = dq8::launch_pad_rows(it.q, (int)it.m, w.k, dst, ldq, s);
+      if (e != hipSuccess) return from_hip(e);
+      q = dst;
+      offset += pad_bytes(w, it.m);
+    }
+    dq8::Proj& p = b.p[b.count++];
+    fill_proj(p, w, q, ldq, it.scales, it.m, it.bias, it.out, dots, it.layout, it.epilogue);
+    p.wave_begin = b.total_waves;
+    if (kind == 0) {
+      p.waves_n = w.np / 64;
+      b.total_waves += p.waves_n * (int)((it.m + 63) / 64);
+    } else {
+      p.waves_n = w.np / 32;
+      b.total_waves += p.waves_n;
+    }
+  }
+  for (int kind = 0; kind < 2; ++kind) {
+    if (batch[kind].count == 0) continue;
+    hipError_t e = dq8::launch_linear(batch[kind], kind, dots != nullptr, s);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  return DQ8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dq8_status_string(dq8_status s) {
+  switch (s) {
+    case DQ8_OK: return "ok";
+    case DQ8_ERR_SHAPE: return "shape mismatch";
+    case DQ8_ERR_NONFINITE: return "non-finite input";
+    case DQ8_ERR_ARG: return "invalid argument";
+    case DQ8_ERR_DEVICE: return "device error";
+    case DQ8_ERR_NOMEM: return "out of device memory";
+  }
+  return "unknown status";
+}
+
+dq8_status dq8_create(int device, dq8_ctx** out) {
+  if (!out) return DQ8_ERR_ARG;
+  *out = nullptr;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return DQ8_ERR_ARG;
+  DeviceGuard guard(device);
+  if (!guard.ok) return DQ8_ERR_DEVICE;
+  dq8_ctx* ctx = new (std::nothrow) dq8_ctx();
+  if (!ctx) return DQ8_ERR_NOMEM;
+  ctx->device = device;
+  hipError_t e = hipMalloc(&ctx->flag, sizeof(uint32_t));
+  if (e != hipSuccess) {
+    delete ctx;
+    return from_hip(e);
+  }
+  *out = ctx;
+  return DQ8_OK;
+}
+
+dq8_status dq8_destroy(dq8_ctx* ctx) {
+  if (!ctx) return DQ8_ERR_ARG;
+  DeviceGuard guard(ctx->device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(ctx->work);
+  (void)hipFree(ctx->flag);
+  delete ctx;
+  return DQ8_OK;
+}
+
+dq8_status dq8_weights_from_quantized(dq8_ctx* ctx, const uint8_t* values, const float* scales, size_t n, size_t k,
+                                      void* stream, dq8_weights** out) {
+  if (!ctx || !values || !scales || !out) return DQ8_ERR_ARG;
+  *out = nullptr;
+  DeviceGuard guard(ctx->device);
+  dq8_weights* h = nullptr;
+  dq8_status st = make_weights(ctx, n, k, &h);
+  if (st != DQ8_OK) return st;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dq8::launch_repack(values, scales, (int)n, (int)k, &h->w, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    dq8_weights_free(h);
+    return from_hip(e);
+  }
+  *out = h;
+  return DQ8_OK;
+}
+
+dq8_status dq8_weights_from_f32(dq8_ctx* ctx, const float* w, size_t n, size_t k, void* stream, dq8_weights** out) {
+  if (!ctx || !w || !out) return DQ8_ERR_ARG;
+  *out = nullptr;
+  if (n == 0 || k == 0 || n > (1u << 30) || k > (1u << 30)) return DQ8_ERR_SHAPE;
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = (hipStream_t)stream;
+  const size_t g = groups_of(k);
+  uint8_t* values = nullptr;
+  float* scales = nullptr;
+  hipError_t e = hipMalloc(&values, n * k);
+  if (e == hipSuccess) e = hipMalloc(&scales, n * g * sizeof(float));
+  // Data::quantize has the same per-group formula as QuantizedInputs::new (weights.rs:117-136).
+  if (e == hipSuccess) e = dq8::launch_quantize(w, (int)n, (int)k, (int8_t*)values, (int)k, scales, nullptr, s);
+  dq8_status st = from_hip(e);
+  if (st == DQ8_OK) st = dq8_weights_from_quantized(ctx, values, scales, n, k, stream, out);
+  (void)hipStreamSynchronize(s);
+  (void)hipFree(values);
+  (void)hipFree(scales);
+  return st;
+}
+
+dq8_status dq8_weights_export(dq8_ctx* ctx, const dq8_weights* w, uint8_t* values, float* scales, void* stream) {
+  if (!ctx || !w || !values || !scales) return DQ8_ERR_ARG;
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dq8::launch_export(&w->w, values, scales, s);
+  return from_hip(e);
+}
+
+dq8_status dq8_weights_shape(const dq8_weights* w, size_t* n, size_t* k) {
+  if (!w || !n || !k) return DQ8_ERR_ARG;
+  *n = (size_t)w->w.n;
+  *k = (size_t)w->w.k;
+  return DQ8_OK;
+}
+
+dq8_status dq8_weights_free(dq8_weights* w) {
+  if (!w) return DQ8_ERR_ARG;
+  DeviceGuard guard(w->w.device);
+  (void)hipDeviceSynchronize();
+  (void)hipFree(w->w.values);
+  (void)hipFree(w->w.scales);
+  delete w;
+  return DQ8_OK;
+}
+
+dq8_status dq8_quantize(dq8_ctx* ctx, const float* x, size_t m, size_t k, int8_t* q, float* scales,
+                        uint32_t* nonfinite, void* stream) {
+  if (!ctx || (m && k && (!x || !q || !scales))) return DQ8_ERR_ARG;
+  if (k == 0 || m > (1u << 30) || k > (1u << 30)) return DQ8_ERR_SHAPE;
+  if (m == 0) return DQ8_OK;
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t* flag = nonfinite ? nonfinite : ctx->flag;
+  hipError_t e = hipSuccess;
+  if (!nonfinite) e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
+  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, (int)k, q, (int)k, scales, flag, s);
+  if (e != hipSuccess) return from_hip(e);
+  if (nonfinite) return DQ8_OK;
+  uint32_t host = 0;
+  e = hipMemcpyAsync(&host, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return from_hip(e);
+  return host ? DQ8_ERR_NONFINITE : DQ8_OK;
+}
+
+dq8_status dq8_linear(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, const float* scales, size_t m,
+                      const float* bias, float* out, dq8_layout layout, dq8_epilogue epilogue, void* stream) {
+  if (!ctx) return DQ8_ERR_ARG;
+  if (m == 0) return w ? DQ8_OK : DQ8_ERR_ARG;
+  dq8_status st = check_item_args(w, q, scales, m, out, layout, epilogue);
+  if (st != DQ8_OK) return st;
+  if (w->w.device != ctx->device) return DQ8_ERR_ARG;
+  DeviceGuard guard(ctx->device);
+  dq8_linear_item it = {w, q, scales, m, bias, out, layout, epilogue};
+  return run_linear(ctx, &it, 1, nullptr, (hipStream_t)stream);
+}
+
+dq8_status dq8_linear_batch(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, void* stream) {
+  if (!ctx || (count && !items)) return DQ8_ERR_ARG;
+  for (size_t i = 0; i < count; ++i) {
+    if (items[i].m == 0) {
+      if (!items[i].w) return DQ8_ERR_ARG;
+      continue;
+    }
+    dq8_status st = check_item_args(items[i].w, items[i].q, items[i].scales, items[i].m, items[i].out,
+                                    items[i].layout, items[i].epilogue);
+    if (st != DQ8_OK) return st;
+    if (items[i].w->w.device != ctx->device) return DQ8_ERR_ARG;
+  }
+  DeviceGuard guard(ctx->device);
+  return run_linear(ctx, items, count, nullptr, (hipStream_t)stream);
+}
+
+dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t m, const float* bias,
+                            float* out, dq8_layout layout, dq8_epilogue epilogue, void* stream) {
+  if (!ctx || !w) return DQ8_ERR_ARG;
+  if (m == 0) return DQ8_OK;
+  if (!x || !out) return DQ8_ERR_ARG;
+  if (layout != DQ8_ROWS && layout != DQ8_COLUMNS) return DQ8_ERR_ARG;
+  if (epilogue != DQ8_WRITE && epilogue != DQ8_ADD && epilogue != DQ8_SWIGLU) return DQ8_ERR_ARG;
+  if (layout == DQ8_COLUMNS && epilogue != DQ8_WRITE) return DQ8_ERR_ARG;
+  if (m > (1u << 30) || w->w.device != ctx->device) return m > (1u << 30) ? DQ8_ERR_SHAPE : DQ8_ERR_ARG;
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = (hipStream_t)stream;
+  const size_t ldq = (size_t)w->w.g * kGroup;
+  const size_t qbytes = (m * ldq + 255) / 256 * 256;
+  dq8_status st = ensure_work(ctx, qbytes + m * w->w.g * sizeof(float));
+  if (st != DQ8_OK) return st;
+  int8_t* q = (int8_t*)ctx->work;
+  float* xs = (float*)((char*)ctx->work + qbytes);
+  hipError_t e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
+  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, w->w.k, q, (int)ldq, xs, ctx->flag, s);
+  uint32_t host = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(&host, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return from_hip(e);
+  if (host) return DQ8_ERR_NONFINITE;
+  dq8::Batch b;
+  b.count = 1;
+  dq8::Proj& p = b.p[0];
+  fill_proj(p, w->w, q, (int)ldq, xs, m, bias, out, nullptr, layout, epilogue);
+  p.wave_begin = 0;
+  const int kind = m <= 32 ? 1 : 0;
+  p.waves_n = kind == 0 ? w->w.np / 64 : w->w.np / 32;
+  b.total_waves = kind == 0 ? p.waves_n * (int)((m + 63) / 64) : p.waves_n;
+  return from_hip(dq8::launch_linear(b, kind, false, s));
+}
+
+dq8_status dq8_group_dots(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, size_t m, int32_t* dots,
+                          void* stream) {
+  if (!ctx || !w || !q || !dots) return DQ8_ERR_ARG;
+  if (m == 0) return DQ8_OK;
+  DeviceGuard guard(ctx->device);
+  // Scales are not read by the dots kernels; pass the weights' own as a valid pointer.
+  dq8_linear_item it = {w, q, w->w.scales, m, nullptr, nullptr, DQ8_ROWS, DQ8_WRITE};
+  return run_linear(ctx, &it, 1, dots, (hipStream_t)stream);
+}
+
+}  // extern "C"

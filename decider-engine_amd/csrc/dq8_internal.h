@@ -1,0 +1,60 @@
+// Internal types shared by the HIP kernels (dq8_kernels.hip) and the C ABI
+// implementation (dq8_api.hip).  Not part of the public interface.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace dq8 {
+
+constexpr int kGroup = 64;        // reference group width (weights.rs:119, tensor.rs:329)
+constexpr int kFragBytes = 1024;  // one MFMA operand fragment: 64 lanes x 16 bytes
+constexpr int kMaxBatch = 16;     // projections per launch
+constexpr int kWaveRows = 64;     // rows per wave in the wide kernel
+constexpr int kColPad = 64;       // weights are padded to a multiple of this many outputs
+
+// Repacked weights, owned by a dq8_weights handle.
+//   values: [Np/32][G][2][64 lanes][16 bytes]; fragment (nb, g, h) holds, at lane l,
+//           output row nb*32 + l%32 and input bytes g*64 + 32h + 16*(l/32) .. +16
+//           (zero beyond N or K).
+//   scales: [G][Np] fp32, group-major (zero beyond N).
+struct Weights {
+  int device;
+  int n, k, g, np;
+  uint8_t* values;
+  float* scales;
+};
+
+// One projection of a launch.  q is [M][ldq] bytes with ldq % 16 == 0 and
+// every byte up to G*64 of each row readable (zero past K).
+struct Proj {
+  const int8_t* q;
+  const float* xs;    // [M][G]
+  const uint8_t* wt;  // Weights::values
+  const float* wst;   // Weights::scales
+  const float* bias;  // [N] or null
+  float* out;
+  int32_t* dots;      // debug output [M][N][G] (dots kernels only)
+  int m, ldq, g, n, np;
+  int epilogue;       // 0 write, 1 add, 2 swiglu
+  int layout;         // 0 rows [M][N], 1 columns [N][M]
+  int wave_begin;     // first wave of this projection in the launch
+  int waves_n;        // column strips of this projection
+};
+
+struct Batch {
+  Proj p[kMaxBatch];
+  int count;
+  int total_waves;
+};
+
+// Kernel launchers (dq8_kernels.hip).  All return hipError_t of the launch.
+hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, float* scales,
+                           uint32_t* nonfinite, hipStream_t s);
+hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int k, Weights* w, hipStream_t s);
+hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipStream_t s);
+hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ldq, hipStream_t s);
+// Kind: 0 wide (M > 32), 1 skinny (M <= 32).  dots selects the debug kernel.
+hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s);
+
+}  // namespace dq8

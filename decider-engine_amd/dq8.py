@@ -1,0 +1,300 @@
+"""Python binding of libdq8.so (include/dq8.h) over ctypes.
+
+Device buffers are torch tensors on a ROCm device (torch is only memory and
+stream plumbing here; every computation runs in the HIP kernels of libdq8.so).
+Work is enqueued on torch's current stream of the tensors' device.
+
+The names mirror decider-engine's int8 path:
+  Weights.from_f32       Data::quantize(Precision::Int8Compute)   weights.rs:98-146
+  Weights.from_quantized Data::Quantized { values, scales, .. }   weights.rs:16-23
+  Context.quantize       QuantizedInputs::new (None -> NonFinite) tensor.rs:315-353
+  Context.linear         linear_int8 + write_columns/Epilogue     tensor.rs:379-456, 272-288
+  Context.linear_f32in   linear (quantize + multiply)             tensor.rs:290-308
+There is no CPU fallback: without libdq8.so, or without a GPU, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+from dataclasses import dataclass
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdq8.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "dq8.h")
+
+OK, ERR_SHAPE, ERR_NONFINITE, ERR_ARG, ERR_DEVICE, ERR_NOMEM = range(6)
+WRITE, ADD, SWIGLU = 0, 1, 2
+ROWS, COLUMNS = 0, 1
+GROUP = 64
+
+
+class Dq8Error(RuntimeError):
+    def __init__(self, status: int, what: str):
+        super().__init__(f"{what}: {status_string(status)} ({status})")
+        self.status = status
+
+
+class NonFinite(Dq8Error):
+    """The reference's `None` from QuantizedInputs::new: the input holds NaN or +-inf."""
+
+
+class _Item(ctypes.Structure):
+    _fields_ = [
+        ("w", ctypes.c_void_p),
+        ("q", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("m", ctypes.c_size_t),
+        ("bias", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("layout", ctypes.c_int),
+        ("epilogue", ctypes.c_int),
+    ]
+
+
+_lib = None
+_vp, _sz, _i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+
+
+def header_functions() -> list[str]:
+    """Every function that include/dq8.h declares."""
+    text = open(HEADER_PATH).read()
+    return sorted(set(re.findall(r"^\s*(?:dq8_status|const char \*)\s*(dq8_\w+)\s*\(", text, re.M)))
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdq8.so (no GPU needed to load it)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"libdq8.so is not built: {LIB_PATH} (run __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    sig = {
+        "dq8_create": ([_i, ctypes.POINTER(_vp)], _i),
+        "dq8_destroy": ([_vp], _i),
+        "dq8_weights_from_f32": ([_vp, _vp, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
+        "dq8_weights_from_quantized": ([_vp, _vp, _vp, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
+        "dq8_weights_export": ([_vp, _vp, _vp, _vp, _vp], _i),
+        "dq8_weights_shape": ([_vp, ctypes.POINTER(_sz), ctypes.POINTER(_sz)], _i),
+        "dq8_weights_free": ([_vp], _i),
+        "dq8_quantize": ([_vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp], _i),
+        "dq8_linear": ([_vp, _vp, _vp, _vp, _sz, _vp, _vp, _i, _i, _vp], _i),
+        "dq8_linear_f32in": ([_vp, _vp, _vp, _sz, _vp, _vp, _i, _i, _vp], _i),
+        "dq8_linear_batch": ([_vp, ctypes.POINTER(_Item), _sz, _vp], _i),
+        "dq8_group_dots": ([_vp, _vp, _vp, _sz, _vp, _vp], _i),
+        "dq8_status_string": ([_i], ctypes.c_char_p),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def status_string(status: int) -> str:
+    try:
+        return lib().dq8_status_string(status).decode()
+    except RuntimeError:
+        return "unknown"
+
+
+def _check(status: int, what: str) -> None:
+    if status == ERR_NONFINITE:
+        raise NonFinite(status, what)
+    if status != OK:
+        raise Dq8Error(status, what)
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device) -> int:
+    torch = _torch()
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def groups(k: int) -> int:
+    return (k + GROUP - 1) // GROUP
+
+
+class Weights:
+    """A repacked int8 weight matrix [n][k] resident on the device."""
+
+    def __init__(self, ctx: "Context", handle: int, n: int, k: int):
+        self.ctx, self.handle, self.n, self.k = ctx, handle, n, k
+
+    @property
+    def groups(self) -> int:
+        return groups(self.k)
+
+    def export(self):
+        """(values uint8 [n][k], scales float32 [n][G]) in the Data::Quantized layout."""
+        torch = _torch()
+        dev = self.ctx.device
+        values = torch.empty((self.n, self.k), dtype=torch.uint8, device=dev)
+        scales = torch.empty((self.n, self.groups), dtype=torch.float32, device=dev)
+        _check(lib().dq8_weights_export(self.ctx.handle, self.handle, values.data_ptr(), scales.data_ptr(),
+                                        _stream(dev)), "dq8_weights_export")
+        return values, scales
+
+    def free(self) -> None:
+        if self.handle:
+            _check(lib().dq8_weights_free(self.handle), "dq8_weights_free")
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+@dataclass
+class Item:
+    """One projection of Context.linear_batch."""
+
+    w: Weights
+    q: object
+    scales: object
+    out: object
+    bias: object = None
+    layout: int = ROWS
+    epilogue: int = WRITE
+
+
+class Context:
+    def __init__(self, device: int = 0):
+        torch = _torch()
+        if not torch.cuda.is_available():
+            raise RuntimeError("dq8 needs a ROCm GPU; none is visible")
+        self.index = device
+        self.device = torch.device("cuda", device)
+        h = ctypes.c_void_p()
+        _check(lib().dq8_create(device, ctypes.byref(h)), "dq8_create")
+        self.handle = h.value
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().dq8_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _dev(self, t, dtype, shape=None, name="tensor"):
+        torch = _torch()
+        if t.device != self.device or t.dtype != dtype or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {dtype} tensor on {self.device}")
+        if shape is not None and tuple(t.shape) != tuple(shape):
+            raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+        return t
+
+    # -- weights -------------------------------------------------------
+    def weights_from_f32(self, w) -> Weights:
+        torch = _torch()
+        self._dev(w, torch.float32, name="w")
+        n, k = w.shape
+        h = ctypes.c_void_p()
+        _check(lib().dq8_weights_from_f32(self.handle, w.data_ptr(), n, k, _stream(self.device), ctypes.byref(h)),
+               "dq8_weights_from_f32")
+        return Weights(self, h.value, n, k)
+
+    def weights_from_quantized(self, values, scales) -> Weights:
+        torch = _torch()
+        self._dev(values, torch.uint8, name="values")
+        n, k = values.shape
+        self._dev(scales, torch.float32, (n, groups(k)), "scales")
+        h = ctypes.c_void_p()
+        _check(lib().dq8_weights_from_quantized(self.handle, values.data_ptr(), scales.data_ptr(), n, k,
+                                                _stream(self.device), ctypes.byref(h)), "dq8_weights_from_quantized")
+        return Weights(self, h.value, n, k)
+
+    # -- activations ---------------------------------------------------
+    def quantize(self, x, q=None, scales=None, nonfinite=None):
+        """QuantizedInputs::new.  Raises NonFinite like the reference's None,
+        unless `nonfinite` (a zeroed int32 device scalar) is given: then the
+        call does not synchronize and the flag is ORed on the device."""
+        torch = _torch()
+        self._dev(x, torch.float32, name="x")
+        m, k = x.shape
+        if q is None:
+            q = torch.empty((m, k), dtype=torch.int8, device=self.device)
+        if scales is None:
+            scales = torch.empty((m, groups(k)), dtype=torch.float32, device=self.device)
+        self._dev(q, torch.int8, (m, k), "q")
+        self._dev(scales, torch.float32, (m, groups(k)), "scales")
+        _check(lib().dq8_quantize(self.handle, x.data_ptr(), m, k, q.data_ptr(), scales.data_ptr(),
+                                  _ptr(nonfinite), _stream(self.device)), "dq8_quantize")
+        return q, scales
+
+    # -- projections ---------------------------------------------------
+    def linear(self, w: Weights, q, scales, out=None, bias=None, layout=ROWS, epilogue=WRITE):
+        torch = _torch()
+        self._dev(q, torch.int8, name="q")
+        m, k = q.shape
+        if k != w.k:
+            raise Dq8Error(ERR_SHAPE, "dq8_linear: input width differs from the weights")
+        self._dev(scales, torch.float32, (m, groups(k)), "scales")
+        shape = (m, w.n) if layout == ROWS else (w.n, m)
+        if out is None:
+            out = torch.zeros(shape, dtype=torch.float32, device=self.device)
+        self._dev(out, torch.float32, shape, "out")
+        if bias is not None:
+            self._dev(bias, torch.float32, (w.n,), "bias")
+        _check(lib().dq8_linear(self.handle, w.handle, q.data_ptr(), scales.data_ptr(), m, _ptr(bias),
+                                out.data_ptr(), layout, epilogue, _stream(self.device)), "dq8_linear")
+        return out
+
+    def linear_f32in(self, w: Weights, x, out=None, bias=None, layout=ROWS, epilogue=WRITE):
+        torch = _torch()
+        self._dev(x, torch.float32, name="x")
+        m, k = x.shape
+        if k != w.k:
+            raise Dq8Error(ERR_SHAPE, "dq8_linear_f32in: input width differs from the weights")
+        shape = (m, w.n) if layout == ROWS else (w.n, m)
+        if out is None:
+            out = torch.zeros(shape, dtype=torch.float32, device=self.device)
+        self._dev(out, torch.float32, shape, "out")
+        if bias is not None:
+            self._dev(bias, torch.float32, (w.n,), "bias")
+        _check(lib().dq8_linear_f32in(self.handle, w.handle, x.data_ptr(), m, _ptr(bias), out.data_ptr(), layout,
+                                      epilogue, _stream(self.device)), "dq8_linear_f32in")
+        return out
+
+    def linear_batch(self, items: list[Item]) -> None:
+        torch = _torch()
+        arr = (_Item * max(1, len(items)))()
+        for i, it in enumerate(items):
+            self._dev(it.q, torch.int8, name="q")
+            m, k = it.q.shape
+            if k != it.w.k:
+                raise Dq8Error(ERR_SHAPE, "dq8_linear_batch: input width differs from the weights")
+            self._dev(it.scales, torch.float32, (m, groups(k)), "scales")
+            shape = (m, it.w.n) if it.layout == ROWS else (it.w.n, m)
+            self._dev(it.out, torch.float32, shape, "out")
+            arr[i] = _Item(it.w.handle, it.q.data_ptr(), it.scales.data_ptr(), m, _ptr(it.bias), it.out.data_ptr(),
+                           it.layout, it.epilogue)
+        _check(lib().dq8_linear_batch(self.handle, arr, len(items), _stream(self.device)), "dq8_linear_batch")
+
+    def group_dots(self, w: Weights, q):
+        torch = _torch()
+        self._dev(q, torch.int8, name="q")
+        m, k = q.shape
+        if k != w.k:
+            raise Dq8Error(ERR_SHAPE, "dq8_group_dots: input width differs from the weights")
+        dots = torch.zeros((m, w.n, groups(k)), dtype=torch.int32, device=self.device)
+        _check(lib().dq8_group_dots(self.handle, w.handle, q.data_ptr(), m, dots.data_ptr(), _stream(self.device)),
+               "dq8_group_dots")
+        return dots

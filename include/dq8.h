@@ -1,0 +1,134 @@
+/*
+ * dq8.h -- C ABI of the MI355X (gfx950) INT8 linear-projection library.
+ *
+ * It is a drop-in for decider-engine's `int8-compute` projection path
+ * (Rust crate decider-engine 0.2.2): group-64 symmetric int8 weights, per-token
+ * group-64 activation quantization, exact i8*i8->i32 group dots and the
+ * group-ordered fp32 rescale-and-sum.  Results are bit-identical to the
+ * crate's CPU path.
+ *
+ * Conventions
+ *   - Every pointer argument is a DEVICE pointer unless named *_host.
+ *   - Callers own activations and outputs; the library owns repacked weights
+ *     (dq8_weights) until dq8_weights_free, and its context workspace.
+ *   - Nothing crosses the ABI as an exception: every entry returns dq8_status.
+ *     Shape errors return DQ8_ERR_SHAPE where the crate panics (assert_eq!).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
+ *     Weight handles are immutable after creation, so calls on different
+ *     streams may share them.  One context must not be used by two host
+ *     threads at once (its workspace is shared by its calls).
+ *   - The library starts no threads.
+ *
+ * Layouts (M tokens, K input width, N outputs, G = ceil(K/64)):
+ *   activations x  fp32 [M][K] row-major        (tensor.rs:315)
+ *   quantized q    int8 [M][K], scales [M][G]   (QuantizedInputs, tensor.rs:310-313)
+ *   weights        u8   [N][K], scales [N][G]   (Data::Quantized, weights.rs:16-23)
+ *   result         fp32 [M][N] row-major        (write_columns, tensor.rs:272-288)
+ *   columns        fp32 [N][M]                  (linear_int8's return, tensor.rs:441-455)
+ */
+#ifndef DQ8_H
+#define DQ8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum dq8_status {
+    DQ8_OK = 0,
+    DQ8_ERR_SHAPE = 1,     /* a size or length disagrees (the crate's assert_eq! panics) */
+    DQ8_ERR_NONFINITE = 2, /* QuantizedInputs::new returned None: caller takes its FP32 path */
+    DQ8_ERR_ARG = 3,       /* null handle/pointer, bad enum value or misaligned pointer */
+    DQ8_ERR_DEVICE = 4,    /* a HIP call failed */
+    DQ8_ERR_NOMEM = 5      /* device allocation failed */
+} dq8_status;
+
+/* Epilogue::{Write, Add, SwiGlu} (tensor.rs:85-100). */
+typedef enum dq8_epilogue { DQ8_WRITE = 0, DQ8_ADD = 1, DQ8_SWIGLU = 2 } dq8_epilogue;
+
+/* Result layout: row-major [M][N] as written by write_columns (tensor.rs:272-288),
+ * or the column-major [N][M] `columns` that linear_int8 returns (tensor.rs:441-455). */
+typedef enum dq8_layout { DQ8_ROWS = 0, DQ8_COLUMNS = 1 } dq8_layout;
+
+typedef struct dq8_ctx dq8_ctx;
+typedef struct dq8_weights dq8_weights;
+
+/* Context on one device.  Replaces the crate's implicit global state
+ * (Kernel::detect, int8.rs:25-30, and the rayon pool). */
+dq8_status dq8_create(int device, dq8_ctx **out);
+dq8_status dq8_destroy(dq8_ctx *ctx);
+
+/* Data::quantize(width, Precision::Int8Compute) (weights.rs:98-146) on the device,
+ * from fp32 weights w [n][k], followed by the one-time repack into the
+ * MFMA fragment layout.  Synchronous with respect to `stream` on return of
+ * the handle (the handle is usable by later work on any stream once `stream`
+ * has progressed past this call; dq8_weights_* calls synchronize `stream`). */
+dq8_status dq8_weights_from_f32(dq8_ctx *ctx, const float *w, size_t n, size_t k, void *stream,
+                                dq8_weights **out);
+
+/* Adopt an existing Data::Quantized { values, scales, width: k, bits: 8 }
+ * (weights.rs:16-23) unchanged: values u8 [n][k] (i8 bit patterns),
+ * scales fp32 [n][ceil(k/64)].  The crate's loader keeps quantizing on the
+ * host; only the repack runs here. */
+dq8_status dq8_weights_from_quantized(dq8_ctx *ctx, const uint8_t *values, const float *scales, size_t n,
+                                      size_t k, void *stream, dq8_weights **out);
+
+/* Write the handle's weights back in the Data::Quantized layout (for checks). */
+dq8_status dq8_weights_export(dq8_ctx *ctx, const dq8_weights *w, uint8_t *values, float *scales,
+                              void *stream);
+dq8_status dq8_weights_shape(const dq8_weights *w, size_t *n, size_t *k);
+dq8_status dq8_weights_free(dq8_weights *w);
+
+/* QuantizedInputs::new (tensor.rs:315-353): per token row, per group of 64,
+ * symmetric absmax int8 and one fp32 scale.  If any element of x is
+ * non-finite the crate returns None (tensor.rs:318-320):
+ *   - nonfinite == NULL: the call synchronizes `stream` and returns
+ *     DQ8_ERR_NONFINITE in that case (q/scales contents are then unspecified);
+ *   - nonfinite != NULL: nothing is synchronized; the kernel ORs 1 into
+ *     *nonfinite (a device uint32 the caller has zeroed) and returns DQ8_OK. */
+dq8_status dq8_quantize(dq8_ctx *ctx, const float *x, size_t m, size_t k, int8_t *q, float *scales,
+                        uint32_t *nonfinite, void *stream);
+
+/* linear_int8 (tensor.rs:379-456) on quantized inputs q [m][k] / scales [m][G]
+ * (a shared QuantizedInputs, tensor.rs:398-402), written through
+ * write_columns + Epilogue (tensor.rs:272-288).  bias may be NULL (the crate adds
+ * +0.0, tensor.rs:437).  For DQ8_COLUMNS the epilogue must be DQ8_WRITE. */
+dq8_status dq8_linear(dq8_ctx *ctx, const dq8_weights *w, const int8_t *q, const float *scales, size_t m,
+                      const float *bias, float *out, dq8_layout layout, dq8_epilogue epilogue, void *stream);
+
+/* `linear` (tensor.rs:290-308) + epilogue: quantize x [m][k] and multiply.
+ * Returns DQ8_ERR_NONFINITE (after synchronizing `stream`), leaving `out`
+ * untouched, where the crate falls back to FP32 (tensor.rs:197-201). */
+dq8_status dq8_linear_f32in(dq8_ctx *ctx, const dq8_weights *w, const float *x, size_t m, const float *bias,
+                            float *out, dq8_layout layout, dq8_epilogue epilogue, void *stream);
+
+/* Several independent projections in one launch (same-shape inputs are not
+ * required).  Each item is one dq8_linear.  This is the shape of a model
+ * layer's projections that read already-available inputs (q/k/v, GDN
+ * qkv/z/b/a, gate/up, or the continuation GEMMs of one question). */
+typedef struct dq8_linear_item {
+    const dq8_weights *w;
+    const int8_t *q;      /* [m][k] int8 */
+    const float *scales;  /* [m][G] */
+    size_t m;
+    const float *bias;    /* NULL: +0.0 */
+    float *out;
+    dq8_layout layout;
+    dq8_epilogue epilogue;
+} dq8_linear_item;
+dq8_status dq8_linear_batch(dq8_ctx *ctx, const dq8_linear_item *items_host, size_t count, void *stream);
+
+/* Debug: every per-group i32 dot, dots [m][n][G], computed by the same MFMA
+ * path as dq8_linear (int8.rs:32-44 per group, as used at tensor.rs:429-436). */
+dq8_status dq8_group_dots(dq8_ctx *ctx, const dq8_weights *w, const int8_t *q, size_t m, int32_t *dots,
+                          void *stream);
+
+/* Human-readable name of a status. */
+const char *dq8_status_string(dq8_status s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DQ8_H */

@@ -1,0 +1,236 @@
+/*
+ * dq8_oracle.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of decider-engine's `int8-compute` projection
+ * arithmetic (Rust crate decider-engine 0.2.2).  It is the checker for the
+ * HIP kernels and the CPU baseline that bench.py times; only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.  The
+ * product library never links, loads or calls it, and it is not a fallback.
+ *
+ * Build: oracle/Makefile (gcc -O3 -ffp-contract=off, no fast-math, default
+ * x86-64 target), so every float operation below is one IEEE-754 binary32
+ * operation with round-to-nearest-even, as rustc emits for the cited Rust.
+ *
+ * Each function names the reference lines it restates.  Pinning (what checks
+ * each function against something other than itself) is listed in the test
+ * module tests/test_oracle.py; every function here is pinned there.
+ */
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define GROUP 64
+
+static size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
+
+/* weights.rs:120-125 and tensor.rs:330-335:
+ *   max = fold(0.0, f32::max, |v|);  scale = max == 0 ? 1 : max(max / bound, f32::MIN_POSITIVE)
+ * f32::max ignores a NaN operand exactly like fmaxf. */
+static float group_scale(const float *v, size_t n, float bound) {
+    float max = 0.0f;
+    for (size_t i = 0; i < n; ++i) max = fmaxf(max, fabsf(v[i]));
+    if (max == 0.0f) return 1.0f;
+    return fmaxf(max / bound, FLT_MIN);
+}
+
+/* weights.rs:129 and tensor.rs:337: (v / scale).round().clamp(-b, b) as i8.
+ * f32::round is half-away-from-zero (C roundf); clamp passes NaN through and
+ * `as i8` maps NaN to 0 (saturating cast). */
+static int8_t quantize_value(float v, float scale, float bound) {
+    float r = roundf(v / scale);
+    if (isnan(r)) return 0;
+    if (r < -bound) r = -bound;
+    if (r > bound) r = bound;
+    return (int8_t)(int)r;
+}
+
+static void quantize_row(const float *row, size_t width, int8_t *q, float *scales) {
+    size_t groups = div_ceil(width, GROUP);
+    for (size_t g = 0; g < groups; ++g) {
+        size_t start = g * GROUP;
+        size_t n = width - start < GROUP ? width - start : GROUP;
+        float s = group_scale(row + start, n, 127.0f);
+        scales[g] = s;
+        for (size_t i = 0; i < n; ++i) q[start + i] = quantize_value(row[start + i], s, 127.0f);
+    }
+}
+
+/* ---------------------------------------------------------------- threads */
+
+typedef void (*range_fn)(void *ctx, size_t begin, size_t end);
+struct range_job { range_fn fn; void *ctx; size_t begin, end; };
+
+static void *range_thread(void *arg) {
+    struct range_job *j = (struct range_job *)arg;
+    j->fn(j->ctx, j->begin, j->end);
+    return NULL;
+}
+
+/* Split [0, n) into `threads` contiguous ranges.  Results never depend on the
+ * split: every output element is computed by exactly one sequential loop, as
+ * with rayon's par_chunks in the reference (tensor.rs:442-448). */
+static void parallel_for(size_t n, int threads, range_fn fn, void *ctx) {
+    if (threads <= 1 || n < 2) { fn(ctx, 0, n); return; }
+    if ((size_t)threads > n) threads = (int)n;
+    pthread_t tid[256];
+    struct range_job jobs[256];
+    if (threads > 256) threads = 256;
+    size_t chunk = div_ceil(n, (size_t)threads);
+    int launched = 0;
+    for (int t = 0; t < threads; ++t) {
+        size_t b = (size_t)t * chunk, e = b + chunk < n ? b + chunk : n;
+        if (b >= e) break;
+        jobs[t] = (struct range_job){fn, ctx, b, e};
+        if (t == 0) continue;
+        if (pthread_create(&tid[t], NULL, range_thread, &jobs[t]) != 0) { fn(ctx, b, e); jobs[t].fn = NULL; }
+        launched = t + 1;
+    }
+    fn(ctx, jobs[0].begin, jobs[0].end);
+    for (int t = 1; t < launched; ++t)
+        if (jobs[t].fn) pthread_join(tid[t], NULL);
+}
+
+/* ------------------------------------------------------------ quantizers */
+
+struct qctx { const float *x; size_t width; int8_t *q; float *scales; };
+static void quantize_rows_range(void *c, size_t b, size_t e) {
+    struct qctx *q = (struct qctx *)c;
+    size_t groups = div_ceil(q->width, GROUP);
+    for (size_t r = b; r < e; ++r)
+        quantize_row(q->x + r * q->width, q->width, q->q + r * q->width, q->scales + r * groups);
+}
+
+/* QuantizedInputs::new (tensor.rs:315-353).  Returns 1 (the reference's None)
+ * when any element of the whole input is non-finite (tensor.rs:318-320), else
+ * 0.  Rows run in parallel only when x.len() >= 65536 (tensor.rs:341). */
+int dq8o_quantize_inputs(const float *x, size_t rows, size_t width, int8_t *q, float *scales, int threads) {
+    size_t n = rows * width;
+    for (size_t i = 0; i < n; ++i)
+        if (!isfinite(x[i])) return 1;
+    struct qctx c = {x, width, q, scales};
+    parallel_for(rows, n >= (1u << 16) ? threads : 1, quantize_rows_range, &c);
+    return 0;
+}
+
+/* Data::quantize for 8 bits (weights.rs:98-146): per output row, per group of
+ * 64, symmetric absmax to [-127, 127]; values are stored as u8 bit patterns
+ * (weights.rs:131), scales row-major [rows][groups]. */
+void dq8o_quantize_weights(const float *w, size_t rows, size_t width, uint8_t *values, float *scales) {
+    size_t groups = div_ceil(width, GROUP);
+    for (size_t r = 0; r < rows; ++r)
+        quantize_row(w + r * width, width, (int8_t *)(values + r * width), scales + r * groups);
+}
+
+/* ------------------------------------------------------------------ dots */
+
+/* scalar_dot (int8.rs:149-154); Kernel::dot asserts len <= 64 (int8.rs:33-36). */
+int32_t dq8o_dot(const int8_t *a, const uint8_t *b, size_t len) {
+    int32_t s = 0;
+    for (size_t i = 0; i < len; ++i) s += (int32_t)a[i] * (int32_t)(int8_t)b[i];
+    return s;
+}
+
+/* Kernel::scaled_dot (int8.rs:53-61): sum = 0.0; for each group in order,
+ * sum += dot as f32 * (x_scale * w_scale) -- three rounded operations. */
+float dq8o_scaled_dot(const int8_t *x, const float *xs, const uint8_t *w, const float *ws, size_t width) {
+    float sum = 0.0f;
+    size_t groups = div_ceil(width, GROUP);
+    for (size_t g = 0; g < groups; ++g) {
+        size_t start = g * GROUP;
+        size_t n = width - start < GROUP ? width - start : GROUP;
+        float p = xs[g] * ws[g];
+        float t = (float)dq8o_dot(x + start, w + start, n) * p;
+        sum = sum + t;
+    }
+    return sum;
+}
+
+/* Every per-group i32 dot, [rows][outputs][groups]: the "i32 accumulators" of
+ * the path (int8.rs:32-44 applied per group as in tensor.rs:429-436). */
+void dq8o_group_dots(const int8_t *q, size_t rows, const uint8_t *w, size_t outputs, size_t width, int32_t *dots) {
+    size_t groups = div_ceil(width, GROUP);
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < outputs; ++c)
+            for (size_t g = 0; g < groups; ++g) {
+                size_t start = g * GROUP;
+                size_t n = width - start < GROUP ? width - start : GROUP;
+                dots[(r * outputs + c) * groups + g] = dq8o_dot(q + r * width + start, w + c * width + start, n);
+            }
+}
+
+/* ---------------------------------------------------------- linear_int8 */
+
+struct lctx {
+    const int8_t *q; const float *xs; size_t rows;
+    const uint8_t *w; const float *ws; size_t width;
+    const float *bias; float *columns;
+};
+/* The per-column closure of linear_int8 (tensor.rs:415-440) without adapter:
+ * for every row, scaled_dot then `sum + bias` with bias 0.0 when absent (437). */
+static void linear_columns_range(void *c, size_t b, size_t e) {
+    struct lctx *l = (struct lctx *)c;
+    size_t groups = div_ceil(l->width, GROUP);
+    for (size_t col = b; col < e; ++col) {
+        const uint8_t *w = l->w + col * l->width;
+        const float *ws = l->ws + col * groups;
+        float bias = l->bias ? l->bias[col] : 0.0f;
+        for (size_t r = 0; r < l->rows; ++r) {
+            float sum = dq8o_scaled_dot(l->q + r * l->width, l->xs + r * groups, w, ws, l->width);
+            l->columns[col * l->rows + r] = sum + bias;
+        }
+    }
+}
+
+/* linear_int8 (tensor.rs:379-456) on already-quantized inputs: output columns
+ * are column-major [outputs][rows]; columns run in parallel when
+ * rows * outputs >= 512 (tensor.rs:442). */
+void dq8o_linear_int8(const int8_t *q, const float *xs, size_t rows, const uint8_t *w, const float *ws,
+                      size_t outputs, size_t width, const float *bias, float *columns, int threads) {
+    struct lctx c = {q, xs, rows, w, ws, width, bias, columns};
+    parallel_for(outputs, rows * outputs >= 512 ? threads : 1, linear_columns_range, &c);
+}
+
+/* qwen.rs:194-199: silu(x) = x * sigmoid(x), sigmoid(x) = 1 / (1 + exp(-x));
+ * f32::exp lowers to the platform libm expf. */
+float dq8o_silu(float x) { return x * (1.0f / (1.0f + expf(-x))); }
+
+/* write_columns (tensor.rs:272-288) with Epilogue::store (tensor.rs:92-99):
+ * 0 Write (dst = v), 1 Add (dst += v), 2 SwiGlu (dst = silu(dst) * v). */
+void dq8o_write_columns(const float *columns, size_t rows, size_t outputs, float *result, int epilogue) {
+    for (size_t r = 0; r < rows; ++r)
+        for (size_t c = 0; c < outputs; ++c) {
+            float v = columns[c * rows + r];
+            float *dst = result + r * outputs + c;
+            if (epilogue == 0) *dst = v;
+            else if (epilogue == 1) *dst = *dst + v;
+            else *dst = dq8o_silu(*dst) * v;
+        }
+}
+
+/* The x86 (non-SDOT) plan of Linear::apply_into_shared (weights.rs:450-491)
+ * without LoRA: `linear` re-quantizes its input (tensor.rs:404), computes the
+ * int8 columns and writes them through the epilogue.  Returns 1 where the
+ * reference falls back to FP32 (non-finite input), leaving `result` as is. */
+int dq8o_linear(const float *x, size_t rows, size_t width, const uint8_t *w, const float *ws, size_t outputs,
+                const float *bias, float *result, int epilogue, int threads) {
+    if (rows == 0) return 0;
+    size_t groups = div_ceil(width, GROUP);
+    size_t nq = rows * width, ns = rows * groups, nc = rows * outputs;
+    int8_t *q = (int8_t *)malloc(nq > 0 ? nq : 1);
+    float *xs = (float *)malloc((ns > 0 ? ns : 1) * sizeof(float));
+    float *columns = (float *)malloc((nc > 0 ? nc : 1) * sizeof(float));
+    int status = 2;
+    if (q && xs && columns) {
+        status = dq8o_quantize_inputs(x, rows, width, q, xs, threads);
+        if (status == 0) {
+            dq8o_linear_int8(q, xs, rows, w, ws, outputs, width, bias, columns, threads);
+            dq8o_write_columns(columns, rows, outputs, result, epilogue);
+        }
+    }
+    free(q); free(xs); free(columns);
+    return status;
+}

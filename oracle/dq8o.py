@@ -1,0 +1,154 @@
+"""TEST INFRASTRUCTURE ONLY -- ctypes binding of the C oracle (dq8_oracle.c).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module; the product library never does.  Arrays are numpy on the
+host.  Build with `make -C oracle` (also done by __graft_entry__.build()).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+GROUP = 64
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libdq8_oracle.so")
+_lib = None
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(dtype=np.int8, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_sz = ctypes.c_size_t
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {_LIB_PATH} (run `make -C oracle`)")
+        L = ctypes.CDLL(_LIB_PATH)
+        L.dq8o_quantize_inputs.argtypes = [_f32p, _sz, _sz, _i8p, _f32p, ctypes.c_int]
+        L.dq8o_quantize_inputs.restype = ctypes.c_int
+        L.dq8o_quantize_weights.argtypes = [_f32p, _sz, _sz, _u8p, _f32p]
+        L.dq8o_quantize_weights.restype = None
+        L.dq8o_dot.argtypes = [_i8p, _u8p, _sz]
+        L.dq8o_dot.restype = ctypes.c_int32
+        L.dq8o_scaled_dot.argtypes = [_i8p, _f32p, _u8p, _f32p, _sz]
+        L.dq8o_scaled_dot.restype = ctypes.c_float
+        L.dq8o_group_dots.argtypes = [_i8p, _sz, _u8p, _sz, _sz, _i32p]
+        L.dq8o_group_dots.restype = None
+        L.dq8o_linear_int8.argtypes = [_i8p, _f32p, _sz, _u8p, _f32p, _sz, _sz, ctypes.c_void_p, _f32p, ctypes.c_int]
+        L.dq8o_linear_int8.restype = None
+        L.dq8o_silu.argtypes = [ctypes.c_float]
+        L.dq8o_silu.restype = ctypes.c_float
+        L.dq8o_write_columns.argtypes = [_f32p, _sz, _sz, _f32p, ctypes.c_int]
+        L.dq8o_write_columns.restype = None
+        L.dq8o_linear.argtypes = [_f32p, _sz, _sz, _u8p, _f32p, _sz, ctypes.c_void_p, _f32p, ctypes.c_int, ctypes.c_int]
+        L.dq8o_linear.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def groups(k: int) -> int:
+    return (k + GROUP - 1) // GROUP
+
+
+def quantize_inputs(x: np.ndarray, threads: int = 1):
+    """QuantizedInputs::new: (q [M][K] int8, scales [M][G]) or None if non-finite."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    q = np.zeros((rows, k), np.int8)
+    s = np.zeros((rows, groups(k)), np.float32)
+    if lib().dq8o_quantize_inputs(x, rows, k, q, s, threads) != 0:
+        return None
+    return q, s
+
+
+def quantize_weights(w: np.ndarray):
+    """Data::quantize (8 bits): (values [N][K] uint8, scales [N][G])."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    n, k = w.shape
+    v = np.zeros((n, k), np.uint8)
+    s = np.zeros((n, groups(k)), np.float32)
+    lib().dq8o_quantize_weights(w, n, k, v, s)
+    return v, s
+
+
+def dot(a: np.ndarray, b: np.ndarray) -> int:
+    a = np.ascontiguousarray(a, dtype=np.int8)
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    assert a.shape == b.shape and a.size <= GROUP
+    return int(lib().dq8o_dot(a, b, a.size))
+
+
+def scaled_dot(x, xs, w, ws) -> np.float32:
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    ws = np.ascontiguousarray(ws, dtype=np.float32)
+    assert x.size == w.size and xs.size == ws.size == groups(x.size)
+    return np.float32(lib().dq8o_scaled_dot(x, xs, w, ws, x.size))
+
+
+def group_dots(q: np.ndarray, w: np.ndarray) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    rows, k = q.shape
+    n = w.shape[0]
+    out = np.zeros((rows, n, groups(k)), np.int32)
+    lib().dq8o_group_dots(q, rows, w, n, k, out)
+    return out
+
+
+def _bias_ptr(bias):
+    if bias is None:
+        return None, None
+    b = np.ascontiguousarray(bias, dtype=np.float32)
+    return b, b.ctypes.data_as(ctypes.c_void_p)
+
+
+def linear_int8(q, xs, w, ws, bias=None, threads: int = 1) -> np.ndarray:
+    """linear_int8 on quantized inputs: columns [N][M]."""
+    q = np.ascontiguousarray(q, dtype=np.int8)
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    ws = np.ascontiguousarray(ws, dtype=np.float32)
+    rows, k = q.shape
+    n = w.shape[0]
+    cols = np.zeros((n, rows), np.float32)
+    keep, bp = _bias_ptr(bias)
+    lib().dq8o_linear_int8(q, xs, rows, w, ws, n, k, bp, cols, threads)
+    return cols
+
+
+def write_columns(columns: np.ndarray, result: np.ndarray, epilogue: int) -> np.ndarray:
+    """write_columns + Epilogue (0 write, 1 add, 2 swiglu) into a copy of result."""
+    columns = np.ascontiguousarray(columns, dtype=np.float32)
+    out = np.array(result, dtype=np.float32, copy=True, order="C")
+    n, rows = columns.shape
+    lib().dq8o_write_columns(columns, rows, n, out, epilogue)
+    return out
+
+
+def silu(x: float) -> np.float32:
+    return np.float32(lib().dq8o_silu(float(x)))
+
+
+def linear(x, w, ws, bias=None, result=None, epilogue: int = 0, threads: int = 1):
+    """The x86 plan of Linear::apply_into (no LoRA): returns result [M][N], or None
+    when the reference would fall back to FP32 (non-finite input)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    ws = np.ascontiguousarray(ws, dtype=np.float32)
+    rows, k = x.shape
+    n = w.shape[0]
+    out = np.zeros((rows, n), np.float32) if result is None else np.array(result, np.float32, copy=True, order="C")
+    keep, bp = _bias_ptr(bias)
+    st = lib().dq8o_linear(x, rows, k, w, ws, n, bp, out, epilogue, threads)
+    if st == 1:
+        return None
+    if st != 0:
+        raise MemoryError("oracle allocation failed")
+    return out

@@ -1,0 +1,273 @@
+"""GPU parity: the HIP path through the C ABI against the oracle, bit for bit.
+
+Quantized int8 tensors, scale bit patterns and per-group i32 dots must be
+identical; fp32 outputs of Write/Add must be identical (the stated tolerance is
+max relative error 1e-6; the kernels meet it exactly).  SwiGlu goes through
+libm expf in the reference and a double-precision exp on the device: its
+tolerance is written in the test.
+"""
+import numpy as np
+import pytest
+import torch
+
+import dq8
+import dq8o
+
+pytestmark = pytest.mark.gpu
+
+FLT_MIN = np.float32(np.finfo(np.float32).tiny)
+SWIGLU_RTOL = 1e-6
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    return a.shape == b.shape and a.tobytes() == b.tobytes()
+
+
+def make_x(rng, rows, width, kind="normal"):
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    if kind == "outliers":
+        ch = rng.choice(width, size=max(1, width // 100), replace=False)
+        x[:, ch] *= np.float32(20.0)
+    elif kind == "student":
+        z = rng.standard_normal((rows, width))
+        chi = rng.chisquare(3, size=(rows, width))
+        x = (z / np.sqrt(chi / 3)).astype(np.float32)
+    elif kind == "edge":
+        x[:, :64] = 0.0  # zero group
+        if width > 64:
+            x[:, 64:min(128, width)] = np.array([1], np.uint32).view(np.float32)[0]  # denormal-only group
+        if width > 130:
+            x[:, 128] = 127.0 * FLT_MIN  # tiny group
+        x[0, -1] = 2.5  # exact half quotients in some groups
+    return x
+
+
+def make_w(rng, n, k):
+    return (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+
+
+# ------------------------------------------------------------ quantization
+
+QUANT_SHAPES = [(1, 1), (3, 63), (2, 64), (5, 65), (7, 100), (4, 131), (19, 255), (3, 256), (9, 257), (128, 2048),
+                (24, 6144), (33, 4097)]
+
+
+@pytest.mark.parametrize("rows,width", QUANT_SHAPES)
+@pytest.mark.parametrize("kind", ["normal", "outliers", "edge", "student"])
+def test_quantize_bit_exact(ctx, rows, width, kind):
+    rng = np.random.default_rng(rows * 7919 + width)
+    x = make_x(rng, rows, width, kind)
+    q, s = ctx.quantize(dev(x))
+    want_q, want_s = dq8o.quantize_inputs(x)
+    assert np.array_equal(host(q), want_q)
+    assert bits_equal(host(s), want_s)
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+def test_quantize_nonfinite_is_reported(ctx, bad):
+    x = np.ones((3, 70), np.float32)
+    x[2, 69] = bad
+    with pytest.raises(dq8.NonFinite):
+        ctx.quantize(dev(x))
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ctx.quantize(dev(x), nonfinite=flag)
+    assert int(host(flag)[0]) == 1
+    flag.zero_()
+    ctx.quantize(dev(np.ones((3, 70), np.float32)), nonfinite=flag)
+    assert int(host(flag)[0]) == 0
+
+
+# ----------------------------------------------------------------- weights
+
+WEIGHT_SHAPES = [(1, 1), (31, 131), (64, 64), (65, 100), (100, 2048), (33, 6144)]
+
+
+@pytest.mark.parametrize("n,k", WEIGHT_SHAPES)
+def test_weights_from_f32_bit_exact_and_export(ctx, n, k):
+    rng = np.random.default_rng(n * 31 + k)
+    w = make_w(rng, n, k)
+    w[0, :min(64, k)] = 0.0
+    h = ctx.weights_from_f32(dev(w))
+    values, scales = h.export()
+    want_v, want_s = dq8o.quantize_weights(w)
+    assert np.array_equal(host(values), want_v)
+    assert bits_equal(host(scales), want_s)
+
+
+@pytest.mark.parametrize("n,k", WEIGHT_SHAPES)
+def test_weights_from_quantized_round_trip(ctx, n, k):
+    rng = np.random.default_rng(n + 17 * k)
+    values = rng.integers(0, 256, size=(n, k), dtype=np.uint8)
+    scales = rng.random((n, -(-k // 64))).astype(np.float32)
+    h = ctx.weights_from_quantized(dev(values), dev(scales))
+    v2, s2 = h.export()
+    assert np.array_equal(host(v2), values)
+    assert bits_equal(host(s2), scales)
+
+
+# -------------------------------------------------------------- group dots
+
+DOT_SHAPES = [(1, 64, 1), (5, 100, 9), (24, 2048, 33), (32, 131, 70), (33, 64, 31), (67, 192, 65), (130, 257, 40)]
+
+
+@pytest.mark.parametrize("m,k,n", DOT_SHAPES)
+def test_group_dots_bit_exact(ctx, m, k, n):
+    rng = np.random.default_rng(m * 1009 + k * 7 + n)
+    values = rng.integers(0, 256, size=(n, k), dtype=np.uint8)
+    values[0, :] = 128  # -128 weights
+    q = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    q[0, :] = -127
+    h = ctx.weights_from_quantized(dev(values), dev(np.ones((n, -(-k // 64)), np.float32)))
+    got = host(ctx.group_dots(h, dev(q)))
+    assert np.array_equal(got, dq8o.group_dots(q, values))
+
+
+def test_group_dots_extremes(ctx):
+    # int8.rs:191-192 through the MFMA path: -128 * 128 and -128 * 127 sums
+    q = np.full((2, 64), -128, np.int8)
+    values = np.stack([np.full(64, 128, np.uint8), np.full(64, 127, np.uint8)])
+    h = ctx.weights_from_quantized(dev(values), dev(np.ones((2, 1), np.float32)))
+    got = host(ctx.group_dots(h, dev(q)))
+    assert got[0, 0, 0] == 1_048_576 and got[0, 1, 0] == -1_040_384
+
+
+# ---------------------------------------------------------------- projection
+
+LINEAR_SHAPES = [(1, 1, 1), (1, 64, 4), (4, 64, 4), (5, 128, 6), (9, 192, 31), (24, 2048, 100), (32, 131, 70),
+                 (33, 100, 9), (67, 128, 8), (64, 2048, 64), (128, 2048, 130), (200, 65, 17), (7, 6144, 33)]
+
+
+@pytest.mark.parametrize("m,k,n", LINEAR_SHAPES)
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_linear_rows_write_bit_exact(ctx, m, k, n, with_bias):
+    rng = np.random.default_rng(m * 131 + k * 3 + n)
+    x = make_x(rng, m, k, "outliers" if k >= 100 else "normal")
+    w = make_w(rng, n, k)
+    bias = rng.standard_normal(n).astype(np.float32) if with_bias else None
+    wv, ws = dq8o.quantize_weights(w)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    out = ctx.linear(h, q, s, bias=None if bias is None else dev(bias))
+    want = dq8o.linear(x, wv, ws, bias=bias, threads=4)
+    assert bits_equal(host(out), want)
+
+
+@pytest.mark.parametrize("m,k,n", [(5, 128, 6), (24, 2048, 100), (67, 128, 8), (130, 257, 40)])
+def test_linear_columns_layout_bit_exact(ctx, m, k, n):
+    rng = np.random.default_rng(m + k + n)
+    x = make_x(rng, m, k)
+    w = make_w(rng, n, k)
+    wv, ws = dq8o.quantize_weights(w)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    cols = ctx.linear(h, q, s, layout=dq8.COLUMNS)
+    qh, sh = dq8o.quantize_inputs(x)
+    assert bits_equal(host(cols), dq8o.linear_int8(qh, sh, wv, ws, threads=4))
+
+
+@pytest.mark.parametrize("m,k,n", [(3, 131, 31), (24, 2048, 64), (67, 192, 65)])
+def test_linear_add_epilogue_bit_exact(ctx, m, k, n):
+    rng = np.random.default_rng(3 * m + k + n)
+    x = make_x(rng, m, k)
+    w = make_w(rng, n, k)
+    prev = rng.standard_normal((m, n)).astype(np.float32)
+    wv, ws = dq8o.quantize_weights(w)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    out = dev(prev)
+    ctx.linear(h, q, s, out=out, epilogue=dq8.ADD)
+    assert bits_equal(host(out), dq8o.linear(x, wv, ws, result=prev, epilogue=1, threads=4))
+
+
+@pytest.mark.parametrize("m,k,n", [(3, 131, 31), (24, 2048, 64), (67, 192, 65)])
+def test_linear_swiglu_epilogue(ctx, m, k, n):
+    rng = np.random.default_rng(5 * m + k + n)
+    x = make_x(rng, m, k)
+    w = make_w(rng, n, k)
+    gate = (rng.standard_normal((m, n)) * 3).astype(np.float32)
+    wv, ws = dq8o.quantize_weights(w)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    out = dev(gate)
+    ctx.linear(h, q, s, out=out, epilogue=dq8.SWIGLU)
+    got = host(out)
+    want = dq8o.linear(x, wv, ws, result=gate, epilogue=2, threads=4)
+    rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
+    assert float(rel.max()) <= SWIGLU_RTOL
+    print(f"swiglu bit-identical fraction {np.mean(got == want):.6f}")
+
+
+def test_linear_f32in_and_nonfinite_fallback(ctx):
+    rng = np.random.default_rng(11)
+    x = make_x(rng, 40, 300)
+    w = make_w(rng, 50, 300)
+    wv, ws = dq8o.quantize_weights(w)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    assert bits_equal(host(ctx.linear_f32in(h, dev(x))), dq8o.linear(x, wv, ws, threads=4))
+    x[3, 7] = np.nan
+    sentinel = dev(np.full((40, 50), 7.0, np.float32))
+    with pytest.raises(dq8.NonFinite):
+        ctx.linear_f32in(h, dev(x), out=sentinel)
+    assert np.all(host(sentinel) == 7.0)  # left untouched for the caller's FP32 path
+
+
+def test_reference_fp64_case_through_gpu(ctx):
+    # tensor.rs:605-662 vectors (first row all zeros, distinct group scales, biases)
+    for width in (1, 15, 16, 17, 63, 64, 65, 131):
+        for rows in (1, 19):
+            output = 31
+            groups = -(-width // 64)
+            x = np.array([0.0 if i < width else ((i * 43 % 255) - 127.0) / 8.0 for i in range(rows * width)],
+                         np.float32).reshape(rows, width)
+            values = np.array([(i * 71 + 128) & 0xFF for i in range(output * width)], np.uint8).reshape(output, width)
+            scales = np.array([(i % 7 + 1) / 32.0 for i in range(output * groups)], np.float32).reshape(output, groups)
+            bias = np.array([i / 16.0 for i in range(output)], np.float32)
+            h = ctx.weights_from_quantized(dev(values), dev(scales))
+            out = ctx.linear_f32in(h, dev(x), bias=dev(bias))
+            assert bits_equal(host(out), dq8o.linear(x, values, scales, bias=bias)), (width, rows)
+
+
+def test_linear_batch_mixed_kinds_matches_single_calls(ctx):
+    rng = np.random.default_rng(99)
+    items, wants = [], []
+    for (m, k, n) in [(24, 2048, 96), (24, 2048, 40), (70, 256, 64), (5, 100, 9), (130, 131, 33)]:
+        x = make_x(rng, m, k)
+        w = make_w(rng, n, k)
+        wv, ws = dq8o.quantize_weights(w)
+        h = ctx.weights_from_quantized(dev(wv), dev(ws))
+        q, s = ctx.quantize(dev(x))
+        out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+        items.append(dq8.Item(h, q, s, out))
+        wants.append(dq8o.linear(x, wv, ws, threads=4))
+    ctx.linear_batch(items)
+    for it, want in zip(items, wants):
+        assert bits_equal(host(it.out), want)
+
+
+def test_config1_single_linear_seed0_bit_exact(ctx):
+    # M=128 tokens, K=2048, N=2048; weights N(0, 0.02^2), activations N(0, 1); seed 0
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((2048, 2048)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((128, 2048)).astype(np.float32)
+    h = ctx.weights_from_f32(dev(w))
+    q, s = ctx.quantize(dev(x))
+    dots = host(ctx.group_dots(h, q))
+    out = host(ctx.linear(h, q, s))
+    wv, ws = dq8o.quantize_weights(w)
+    qh, sh = dq8o.quantize_inputs(x)
+    assert np.array_equal(host(q), qh) and bits_equal(host(s), sh)
+    ev, es = h.export()
+    assert np.array_equal(host(ev), wv) and bits_equal(host(es), ws)
+    assert np.array_equal(dots, dq8o.group_dots(qh, wv))
+    assert bits_equal(out, dq8o.linear(x, wv, ws, threads=8))

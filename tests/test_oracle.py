@@ -1,0 +1,340 @@
+"""Pins the oracle (C restatement, oracle/dq8_oracle.c) without a GPU.
+
+Each oracle function is checked against something other than itself:
+  * the reference's own test vectors and known answers (int8.rs:172-297,
+    tensor.rs:605-803, weights.rs:841-866), restated here as data/formulas;
+  * an independent numpy restatement (oracle/oracle_np.py), bit for bit;
+  * a pure-Python scalar emulation of binary32 arithmetic (each operation
+    computed exactly in double and rounded to float32 -- exact for a single
+    +, * of two float32 values);
+  * closed forms (round-half-away ties, FLT_MIN floor, zero groups).
+Planted mistakes (half-to-even rounding, a fused multiply-add, reversed group
+order, a transposed weight row) are applied to the numpy restatement and must
+fail these checks, so the checks can tell a wrong oracle from a right one.
+"""
+import struct
+
+import numpy as np
+import pytest
+
+import dq8o
+import oracle_np as onp
+
+F32 = np.float32
+FLT_MIN = np.float32(np.finfo(np.float32).tiny)
+
+
+def f32(v: float) -> float:
+    return struct.unpack("f", struct.pack("f", v))[0]
+
+
+def py_scaled_dot(x, xs, w, ws):
+    """Scalar emulation of Kernel::scaled_dot (int8.rs:53-61)."""
+    s = 0.0
+    for g in range(len(xs)):
+        d = 0
+        for k in range(64 * g, min(64 * g + 64, len(x))):
+            d += int(x[k]) * int(np.int8(np.uint8(w[k]).view(np.int8)))
+        p = f32(float(xs[g]) * float(ws[g]))
+        t = f32(float(d) * p)
+        s = f32(s + t)
+    return s
+
+
+def py_quantize_group(vals):
+    """Scalar emulation of one group (tensor.rs:330-338)."""
+    m = 0.0
+    for v in vals:
+        m = max(m, abs(float(v)))
+    scale = 1.0 if m == 0.0 else max(f32(m / 127.0), float(FLT_MIN))
+    out = []
+    for v in vals:
+        r = f32(float(v) / scale)
+        q = np.sign(r) * np.floor(abs(r) + 0.5)
+        out.append(int(min(max(q, -127.0), 127.0)))
+    return f32(scale), out
+
+
+# ----------------------------------------------------------- int8.rs tests
+
+
+def test_dot_all_lengths_match_integer_reference():
+    # int8.rs:177-190: lengths 0..=64, unaligned starts, -128 and 127 present
+    for length in range(65):
+        a = np.array([(i * 71 + 128) & 0xFF for i in range(length + 1)], np.uint8).view(np.int8)
+        b = np.array([(i * 37 + 128) & 0xFF for i in range(length + 1)], np.uint8)
+        expected = sum(int(a[i]) * int(b[i:i + 1].view(np.int8)[0]) for i in range(1, length + 1))
+        assert dq8o.dot(a[1:], b[1:]) == expected
+
+
+def test_dot_extremes_known_answers():
+    # int8.rs:191-192
+    assert dq8o.dot(np.full(64, -128, np.int8), np.full(64, 128, np.uint8)) == 1_048_576
+    assert dq8o.dot(np.full(64, -128, np.int8), np.full(64, 127, np.uint8)) == -1_040_384
+
+
+def _tile_case(width):
+    groups = -(-width // 64)
+
+    def bytes_(seed):
+        return np.array([(i * 73 + seed * 151) % 256 for i in range(width)], np.uint8)
+
+    def scales(seed):
+        out = []
+        for g in range(groups):
+            k = (g + seed) % 5
+            out.append(1e-30 if k == 0 else 3.5e6 if k == 1 else (k + seed / 7.0) / 113.0)
+        return np.array(out, np.float32)
+
+    xs = [bytes_(r).view(np.int8) for r in range(4)]
+    ws = [bytes_(c) for c in range(4, 8)]
+    x_scales = [scales(r) for r in range(4)]
+    w_scales = [scales(c) for c in range(4, 8)]
+    return xs, x_scales, ws, w_scales
+
+
+@pytest.mark.parametrize("width", [64, 128, 192, 2048, 100, 1])
+def test_scaled_dot_matches_scalar_emulation_on_tile_vectors(width):
+    # int8.rs:195-237 data; every (row, column) pair against the scalar emulation
+    xs, x_scales, ws, w_scales = _tile_case(width)
+    for r in range(4):
+        for c in range(4):
+            got = dq8o.scaled_dot(xs[r], x_scales[r], ws[c], w_scales[c])
+            want = py_scaled_dot(xs[r], x_scales[r], ws[c], w_scales[c])
+            assert struct.pack("f", got) == struct.pack("f", want), (width, r, c)
+
+
+def test_scaled_tile_extremes_known_answer():
+    # int8.rs:238-263: every product (-128)(-128) or 127(-128); scales [1.0, 0.5]
+    x = [np.full(128, -128, np.int8), np.full(128, 127, np.int8), np.full(128, -128, np.int8),
+         np.zeros(128, np.int8)]
+    w = [np.full(128, 128, np.uint8), np.full(128, 128, np.uint8), np.full(128, 127, np.uint8),
+         np.full(128, 1, np.uint8)]
+    s = np.array([1.0, 0.5], np.float32)
+    assert dq8o.scaled_dot(x[0], s, w[0], s) == 64.0 * 16384.0 * 1.0 + 64.0 * 16384.0 * 0.25
+    for r in range(4):
+        for c in range(4):
+            assert dq8o.scaled_dot(x[r], s, w[c], s) == np.float32(py_scaled_dot(x[r], s, w[c], s))
+
+
+# --------------------------------------------------------- tensor.rs tests
+
+
+@pytest.mark.parametrize("width", [1, 15, 16, 17, 63, 64, 65, 131])
+@pytest.mark.parametrize("rows", [1, 19])
+def test_integer_projection_matches_independent_fp64_reference(width, rows):
+    # tensor.rs:605-662 (bias included)
+    output = 31
+    groups = -(-width // 64)
+    x = np.array([0.0 if i < width else ((i * 43 % 255) - 127.0) / 8.0 for i in range(rows * width)],
+                 np.float32).reshape(rows, width)
+    values = np.array([(i * 71 + 128) & 0xFF for i in range(output * width)], np.uint8).reshape(output, width)
+    scales = np.array([(i % 7 + 1) / 32.0 for i in range(output * groups)], np.float32).reshape(output, groups)
+    bias = np.array([i / 16.0 for i in range(output)], np.float32)
+    actual = dq8o.linear(x, values, scales, bias=bias)
+    q, xs = dq8o.quantize_inputs(x)
+    wdeq = values.view(np.int8).astype(np.float64) * np.repeat(scales.astype(np.float64), 64, axis=1)[:, :width]
+    for column in range(output):
+        for row in range(rows):
+            exp = float(bias[column]) + sum(
+                float(wdeq[column, k]) * float(q[row, k]) * float(xs[row, k // 64]) for k in range(width))
+            assert abs(float(actual[row, column]) - exp) < 1e-3 + abs(exp) * 1e-6
+
+
+@pytest.mark.parametrize("rows,width,output", [(1, 64, 4), (4, 64, 4), (5, 128, 6), (9, 192, 31), (67, 128, 8),
+                                               (7, 100, 9)])
+def test_projection_columns_match_per_output_scaled_dots(rows, width, output):
+    # tensor.rs:664-732 without the LoRA adapter: columns == scaled_dot + bias, bitwise
+    groups = -(-width // 64)
+    x = np.array([((i * 43 % 255) - 127.0) / 9.0 for i in range(rows * width)], np.float32).reshape(rows, width)
+    values = np.array([(i * 71 + 128) & 0xFF for i in range(output * width)], np.uint8).reshape(output, width)
+    scales = np.array([(i % 7 + 1) / 32.0 for i in range(output * groups)], np.float32).reshape(output, groups)
+    bias = np.array([i / 16.0 - 0.5 for i in range(output)], np.float32)
+    q, xs = dq8o.quantize_inputs(x)
+    cols = dq8o.linear_int8(q, xs, values, scales, bias=bias, threads=4)
+    for column in range(output):
+        for row in range(rows):
+            want = np.float32(dq8o.scaled_dot(q[row], xs[row], values[column], scales[column]) + bias[column])
+            assert cols[column, row].tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("rows,width", [(3, 100), (70, 1000), (40, 2048)])
+def test_parallel_input_quantization_matches_serial(rows, width):
+    # tensor.rs:734-766
+    def val(i):
+        k = i % 17
+        return 0.0 if k == 0 else -1e-38 if k == 1 else ((i * 31 % 499) - 249.0) / k
+
+    x = np.array([val(i) for i in range(rows * width)], np.float32).reshape(rows, width)
+    a = dq8o.quantize_inputs(x, threads=1)
+    b = dq8o.quantize_inputs(x, threads=4)
+    assert np.array_equal(a[0], b[0])
+    assert a[1].tobytes() == b[1].tobytes()
+    assert a[1].shape == (rows, -(-width // 64))
+
+
+def test_input_quantization_error_bound_zero_and_denormal_groups_and_nonfinite():
+    # tensor.rs:768-803
+    width = 131
+    x = np.array([((i % 79) - 39.0) / 11.0 for i in range(width * 3)], np.float32)
+    x[:64] = 0.0
+    x[64:128] = np.array([1], np.uint32).view(np.float32)[0]
+    x = x.reshape(3, width)
+    q, s = dq8o.quantize_inputs(x)
+    assert s.shape == (3, 3)
+    assert s[0, 0] == 1.0  # zero group: scale 1.0 (tensor.rs:331-332)
+    assert s[0, 1] == FLT_MIN  # denormal-only group: floor at f32::MIN_POSITIVE
+    for row in range(3):
+        for g in range(3):
+            scale = s[row, g]
+            assert np.isfinite(scale) and scale > 0
+            for k in range(64 * g, min(64 * g + 64, width)):
+                restored = np.float32(q[row, k]) * scale
+                assert abs(float(restored) - float(x[row, k])) <= float(scale) / 2 + 1e-6
+    for bad in (np.nan, np.inf, -np.inf):
+        assert dq8o.quantize_inputs(np.array([[bad]], np.float32)) is None
+        assert dq8o.linear(np.array([[bad]], np.float32), np.array([[1]], np.uint8),
+                           np.array([[1.0]], np.float32)) is None
+
+
+def test_weight_quantization_error_bound_partial_groups_and_zero_rows():
+    # weights.rs:841-866 (8-bit bound 127)
+    width = 131
+    w = np.array([0.0 if i < width else ((i % 113) - 56.0) / 19.0 for i in range(width * 3)],
+                 np.float32).reshape(3, width)
+    values, scales = dq8o.quantize_weights(w)
+    restored = values.view(np.int8).astype(np.float32) * np.repeat(scales, 64, axis=1)[:, :width]
+    for r in range(3):
+        for g in range(3):
+            blk = slice(64 * g, min(64 * g + 64, width))
+            m = np.abs(w[r, blk]).max()
+            assert np.all(np.abs(w[r, blk] - restored[r, blk]) <= m / (2 * 127.0) + 1e-6)
+    assert np.all(scales[0] == 1.0)
+
+
+def test_benchmark_inputs_formula_projection():
+    # tensor.rs:553-603 inputs (weights ((i*71 % 255) - 127) as u8, scales 1/127;
+    # x = ((i*43 % 255) - 127) / 127) at a reduced width: oracle == numpy == scalar emulation
+    width, output, rows = 256, 8, 3
+    values = np.array([((i * 71 % 255) - 127) & 0xFF for i in range(width * output)], np.uint8).reshape(output, width)
+    scales = np.full((output, width // 64), 1.0 / 127.0, np.float32)
+    x = np.array([((i * 43 % 255) - 127.0) / 127.0 for i in range(rows * width)], np.float32).reshape(rows, width)
+    got = dq8o.linear(x, values, scales)
+    q, xs = dq8o.quantize_inputs(x)
+    for r in range(rows):
+        for c in range(output):
+            assert np.float32(got[r, c]) == np.float32(py_scaled_dot(q[r], xs[r], values[c], scales[c]) + 0.0)
+
+
+# ------------------------------------------------------------ closed forms
+
+
+def test_quantize_closed_forms_round_half_away_and_floors():
+    # A group whose absmax is 127 has scale exactly 1.0, so q = round(v) half away from zero.
+    g = np.zeros(64, np.float32)
+    g[:8] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5, 126.5, -126.49999]
+    q, s = dq8o.quantize_inputs(g[None, :])
+    assert s[0, 0] == 1.0
+    assert list(q[0, :8]) == [127, 3, -3, 1, -1, 2, 127, -126]
+    # Absmax below 127 * FLT_MIN: the scale floors at FLT_MIN and q = round(v / FLT_MIN).
+    tiny = np.zeros(64, np.float32)
+    tiny[0] = np.float32(100) * FLT_MIN
+    tiny[1] = np.float32(-3.5) * FLT_MIN
+    q, s = dq8o.quantize_inputs(tiny[None, :])
+    assert s[0, 0] == FLT_MIN and q[0, 0] == 100 and q[0, 1] == -4
+    # A scalar emulation of one group agrees on random data, including ties.
+    rng = np.random.default_rng(7)
+    for trial in range(50):
+        vals = (rng.integers(-600, 600, size=64) / 4.0).astype(np.float32)  # many exact .5 quotients
+        if trial % 2:
+            vals = rng.standard_normal(64).astype(np.float32) * np.float32(10.0 ** rng.integers(-30, 30))
+        q, s = dq8o.quantize_inputs(vals[None, :])
+        scale, qs = py_quantize_group(vals)
+        assert s[0, 0] == np.float32(scale) and list(q[0]) == qs
+
+
+def test_linear_with_zero_rows_is_a_no_op():
+    out = dq8o.linear(np.zeros((0, 64), np.float32), np.zeros((3, 64), np.uint8), np.ones((3, 1), np.float32))
+    assert out.shape == (0, 3)
+
+
+# ------------------------------------------------------ C == numpy, bitwise
+
+
+def _random_case(rng, rows, width, output, outliers=False):
+    x = rng.standard_normal((rows, width)).astype(np.float32)
+    if outliers:
+        ch = rng.choice(width, size=max(1, width // 100), replace=False)
+        x[:, ch] *= np.float32(20.0)
+    w = (rng.standard_normal((output, width)) * 0.02).astype(np.float32)
+    return x, w
+
+
+@pytest.mark.parametrize("rows,width,output", [(1, 1, 1), (3, 63, 5), (19, 64, 31), (7, 65, 9), (33, 131, 17),
+                                               (24, 2048, 40), (5, 6144, 7)])
+def test_c_oracle_matches_numpy_restatement_bitwise(rows, width, output):
+    rng = np.random.default_rng(rows * 1000 + width)
+    x, w = _random_case(rng, rows, width, output, outliers=width >= 100)
+    cv, cs = dq8o.quantize_weights(w)
+    nq, ns = onp.quantize(w)
+    assert np.array_equal(cv.view(np.int8), nq) and cs.tobytes() == ns.tobytes()
+    cq, cxs = dq8o.quantize_inputs(x, threads=4)
+    nxq, nxs = onp.quantize_inputs(x)
+    assert np.array_equal(cq, nxq) and cxs.tobytes() == nxs.tobytes()
+    assert np.array_equal(dq8o.group_dots(cq, cv), onp.group_dots(nxq, cv))
+    bias = rng.standard_normal(output).astype(np.float32)
+    cols = dq8o.linear_int8(cq, cxs, cv, cs, bias=bias, threads=3)
+    rows_np = onp.linear_rows(nxq, nxs, cv, cs, bias=bias)
+    assert cols.T.tobytes() == np.ascontiguousarray(rows_np).tobytes()
+    for ep in (0, 1, 2):
+        prev = rng.standard_normal((rows, output)).astype(np.float32)
+        c_out = dq8o.linear(x, cv, cs, bias=bias, result=prev, epilogue=ep, threads=2)
+        n_out = onp.store(prev, rows_np, ep)
+        assert c_out.tobytes() == np.ascontiguousarray(n_out).tobytes()
+
+
+# ----------------------------------------------------------- planted faults
+
+
+def _mutant_rescale(kind):
+    def fn(dots, xs, ws, bias=None):
+        rows, n, g = dots.shape
+        s = np.zeros((rows, n), np.float32)
+        order = range(g - 1, -1, -1) if kind == "reversed" else range(g)
+        for gi in order:
+            p = xs[:, gi][:, None] * ws[:, gi][None, :]
+            if kind == "fma":
+                s = (s.astype(np.float64) + dots[:, :, gi].astype(np.float64) * p.astype(np.float64)).astype(np.float32)
+            else:
+                s = s + dots[:, :, gi].astype(np.float32) * p
+        return s
+    return fn
+
+
+@pytest.mark.parametrize("kind", ["reversed", "fma"])
+def test_planted_rescale_faults_are_detected(kind):
+    xs, x_scales, ws, w_scales = _tile_case(2048)
+    q = np.stack(xs)
+    w = np.stack(ws)
+    dots = onp.group_dots(q, w)
+    right = onp.rescale_sum(dots, np.stack(x_scales), np.stack(w_scales))
+    wrong = _mutant_rescale(kind)(dots, np.stack(x_scales), np.stack(w_scales))
+    emu = np.array([[py_scaled_dot(xs[r], x_scales[r], ws[c], w_scales[c]) for c in range(4)] for r in range(4)],
+                   np.float32)
+    assert right.tobytes() == emu.tobytes()
+    assert wrong.tobytes() != emu.tobytes()
+
+
+def test_planted_rounding_and_transpose_faults_are_detected():
+    g = np.zeros(64, np.float32)
+    g[:4] = [127.0, 2.5, -2.5, 0.5]
+    half_even = np.clip(np.round(g), -127, 127).astype(np.int8)  # np.round is half-to-even
+    q, _ = dq8o.quantize_inputs(g[None, :])
+    assert not np.array_equal(half_even, q[0])
+    # A transposed weight layout gives different dots on the tensor.rs:664 data.
+    x = np.array([((i * 43 % 255) - 127.0) / 9.0 for i in range(5 * 128)], np.float32).reshape(5, 128)
+    values = np.array([(i * 71 + 128) & 0xFF for i in range(6 * 128)], np.uint8).reshape(6, 128)
+    qx, _ = dq8o.quantize_inputs(x)
+    right = dq8o.group_dots(qx, values)
+    wrong = onp.group_dots(qx, np.ascontiguousarray(values.reshape(128, 6).T))
+    assert not np.array_equal(right, wrong)
