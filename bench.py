@@ -1,0 +1,413 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X int8 projection path (one JSON line on stdout).
+
+Headline workload (a "step"): the full projection stack of a 24-layer,
+2048-hidden model for one 2048-token prefill -- 18 Gated DeltaNet layers and 6
+GQA layers in D,D,D,F order, each followed by a 2048<->6144 SwiGLU FFN:
+  GDN  in 2048->8224 (q,k,v,z + b,a concatenated), out 2048->2048
+  GQA  q 2048->2048, k 2048->512, v 2048->512 (one grouped launch), o 2048->2048
+  FFN  gate 2048->6144 (Write), up 2048->6144 (SwiGlu into gate),
+       down 6144->2048 (Add into the residual) on the re-quantized gate
+Every projection input is quantized inside the step (as the reference's timed
+region does); weights are repacked once before timing.  Weights ~N(0, 0.02^2),
+activations Student-t(3), seeded; all inputs are resident in HBM.
+
+Secondary workload (reported under "skinny"): 16 questions x 24 tokens, each
+question one grouped skinny launch over one layer's projection set (q, k, v, o,
+GDN in/out, FFN gate/up/down), rotating 5 weight copies (> 256 MB MALL) so
+weight bytes come from HBM.
+
+"roofline" is for the dominant kernel (the wide projection kernel): achieved
+= algorithmic int8 ops per launch / its average launch time from HIP events on
+the launch stream.  "cpu_baseline" times the oracle (the C restatement of the
+reference's x86 path) on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "decider-engine_amd"))
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0    # MI355X HBM3E, 8 TB/s
+HIDDEN, FFN_DIM, GDN_IN = 2048, 6144, 4 * 2048 + 2 * 16
+LAYER_KINDS = ["gdn", "gdn", "gdn", "gqa"] * 6
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--tokens", type=int, default=2048)
+    p.add_argument("--questions", type=int, default=16)
+    p.add_argument("--question-tokens", type=int, default=24)
+    p.add_argument("--weight-copies", type=int, default=5)
+    p.add_argument("--skinny-reps", type=int, default=10)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run a plain 1 GiB device copy (for rocprof counter calibration)")
+    return p.parse_args()
+
+
+def student_t(torch, gen, shape, device):
+    z = torch.randn(shape, generator=gen, device=device)
+    chi = (torch.randn((3,) + tuple(shape), generator=gen, device=device) ** 2).sum(0)
+    return (z / torch.sqrt(chi / 3.0)).contiguous()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import dq8
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.add(src, 0.0, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": src.numel() * 4, "bytes_written": dst.numel() * 4}))
+        return
+    ctx = dq8.Context(0)
+    lib = dq8.lib()
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+
+    def weights(n, k):
+        w = (torch.randn((n, k), generator=gen, device=dev) * 0.02).contiguous()
+        h = ctx.weights_from_f32(w)
+        del w
+        return h
+
+    M = args.tokens
+    # ---------------------------------------------------------- the stack
+    layers = []
+    for kind in LAYER_KINDS:
+        L = {"kind": kind}
+        if kind == "gdn":
+            L["in"] = weights(GDN_IN, HIDDEN)
+            L["out"] = weights(HIDDEN, HIDDEN)
+        else:
+            L["q"] = weights(HIDDEN, HIDDEN)
+            L["k"] = weights(512, HIDDEN)
+            L["v"] = weights(512, HIDDEN)
+            L["o"] = weights(HIDDEN, HIDDEN)
+        L["gate"] = weights(FFN_DIM, HIDDEN)
+        L["up"] = weights(FFN_DIM, HIDDEN)
+        L["down"] = weights(HIDDEN, FFN_DIM)
+        L["x"] = student_t(torch, gen, (M, HIDDEN), dev)      # mixer input
+        L["mix"] = student_t(torch, gen, (M, HIDDEN), dev)    # attention / recurrence output
+        L["ffn"] = student_t(torch, gen, (M, HIDDEN), dev)    # post-norm FFN input
+        layers.append(L)
+    groups = lambda k: (k + 63) // 64
+    qx = torch.empty((M, HIDDEN), dtype=torch.int8, device=dev)
+    sx = torch.empty((M, groups(HIDDEN)), dtype=torch.float32, device=dev)
+    qf = torch.empty((M, FFN_DIM), dtype=torch.int8, device=dev)
+    sf = torch.empty((M, groups(FFN_DIM)), dtype=torch.float32, device=dev)
+    mixer_out = torch.empty((M, GDN_IN), dtype=torch.float32, device=dev)
+    k_out = torch.empty((M, 512), dtype=torch.float32, device=dev)
+    v_out = torch.empty((M, 512), dtype=torch.float32, device=dev)
+    proj_out = torch.empty((M, HIDDEN), dtype=torch.float32, device=dev)
+    gate = torch.empty((M, FFN_DIM), dtype=torch.float32, device=dev)
+    resid = torch.zeros((M, HIDDEN), dtype=torch.float32, device=dev)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def quant(x, q, s, k):
+        return ("quant", lib.dq8_quantize, (ctx.handle, x.data_ptr(), M, k, q.data_ptr(), s.data_ptr(),
+                                            flag.data_ptr(), sh), (M * k * 4 + M * k + M * groups(k) * 4, 0))
+
+    def linear(w, q, s, out, ep):
+        return ("linear", lib.dq8_linear, (ctx.handle, w.handle, q.data_ptr(), s.data_ptr(), M, None,
+                                           out.data_ptr(), dq8.ROWS, ep, sh), (0, 2 * M * w.n * w.k))
+
+    calls = []
+    for L in layers:
+        calls.append(quant(L["x"], qx, sx, HIDDEN))
+        if L["kind"] == "gdn":
+            calls.append(linear(L["in"], qx, sx, mixer_out, dq8.WRITE))
+        else:
+            items = (dq8._Item * 3)()
+            outs = (mixer_out, k_out, v_out)
+            for i, name in enumerate(("q", "k", "v")):
+                items[i] = dq8._Item(L[name].handle, qx.data_ptr(), sx.data_ptr(), M, None, outs[i].data_ptr(),
+                                     dq8.ROWS, dq8.WRITE)
+            L["items"] = items
+            flops = sum(2 * M * L[n].n * L[n].k for n in ("q", "k", "v"))
+            calls.append(("linear", lib.dq8_linear_batch, (ctx.handle, items, 3, sh), (0, flops)))
+        calls.append(quant(L["mix"], qx, sx, HIDDEN))
+        calls.append(linear(L["out"] if L["kind"] == "gdn" else L["o"], qx, sx, proj_out, dq8.WRITE))
+        calls.append(quant(L["ffn"], qx, sx, HIDDEN))
+        calls.append(linear(L["gate"], qx, sx, gate, dq8.WRITE))
+        calls.append(linear(L["up"], qx, sx, gate, dq8.SWIGLU))
+        calls.append(quant(gate, qf, sf, FFN_DIM))
+        calls.append(linear(L["down"], qf, sf, resid, dq8.ADD))
+    step_ops = sum(c[3][1] for c in calls)
+
+    def run_step(events=None):
+        for i, (kind, fn, a, _) in enumerate(calls):
+            if events is not None:
+                events[i][0].record(stream)
+            st = fn(*a)
+            if st != 0:
+                raise dq8.Dq8Error(st, fn.__name__)
+            if events is not None:
+                events[i][1].record(stream)
+
+    for _ in range(args.warmup):
+        run_step()
+    torch.cuda.synchronize()
+    if int(flag.item()) != 0:
+        raise RuntimeError("synthetic activations were reported non-finite")
+    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in calls]
+          for _ in range(args.steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for s in range(args.steps):
+        run_step(ev[s])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_total = t0.elapsed_time(t1)
+    ms_step = ms_total / args.steps
+    lin_ms = quant_ms = 0.0
+    lin_n = quant_n = 0
+    quant_bytes = sum(c[3][0] for c in calls if c[0] == "quant")
+    for s in range(args.steps):
+        for i, c in enumerate(calls):
+            d = ev[s][i][0].elapsed_time(ev[s][i][1])
+            if c[0] == "linear":
+                lin_ms += d
+                lin_n += 1
+            else:
+                quant_ms += d
+                quant_n += 1
+    lin_ops_per_launch = sum(c[3][1] for c in calls if c[0] == "linear") / sum(1 for c in calls if c[0] == "linear")
+    lin_avg_ms = lin_ms / lin_n
+    achieved = lin_ops_per_launch / (lin_avg_ms * 1e-3) / 1e12
+    value = step_ops / (ms_step * 1e-3) / 1e12
+
+    # release the stack before the skinny workload
+    for L in layers:
+        for key in ("in", "out", "q", "k", "v", "o", "gate", "up", "down"):
+            if key in L:
+                L[key].free()
+    del layers, calls, ev
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+    skinny = run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen)
+    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, torch, dq8, ctx, dev, gen)
+    traffic = load_traffic("linear_wide_stack2048")
+    out = {
+        "metric": "int8 prefill-projection TOPS (% of i8 MFMA peak); skinny-M HBM GB/s",
+        "value": round(value, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i8",
+        "data": "synthetic (seeded; weights N(0,0.02^2) per-row group-64 int8, activations Student-t(3))",
+        "config": {
+            "workload": "24-layer projection stack, one 2048-token prefill (18 GDN + 6 GQA, each + 2048<->6144 "
+                        "SwiGLU FFN), input quantization included",
+            "tokens": M,
+            "hidden": HIDDEN,
+            "ops_per_step": step_ops,
+            "frac_of_int8_peak": round(value / PEAK_INT8_TOPS, 4),
+            "quantize_ms_per_step": round(quant_ms / args.steps, 4),
+            "quantize_gbs": round(quant_bytes * args.steps / (quant_ms * 1e-3) / 1e9, 1),
+            "projection_ms_per_step": round(lin_ms / args.steps, 4),
+        },
+        "roofline": {
+            "kernel": "k_linear_wide",
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_INT8_TOPS,
+            "unit": "TOP/s",
+            "frac": round(achieved / PEAK_INT8_TOPS, 4),
+            "traffic": traffic,
+            "ops_per_launch": lin_ops_per_launch,
+            "avg_launch_ms": round(lin_avg_ms, 5),
+        },
+        "skinny": skinny,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
+    """16 questions x M tokens, one grouped launch per question over a layer's projections."""
+    M = args.question_tokens
+    shapes = [("q", HIDDEN, HIDDEN), ("k", 512, HIDDEN), ("v", 512, HIDDEN), ("o", HIDDEN, HIDDEN),
+              ("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN), ("gate", FFN_DIM, HIDDEN),
+              ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
+    wbytes = sum(n * k + 4 * n * ((k + 63) // 64) for _, n, k in shapes)
+    copies = []
+    for _ in range(args.weight_copies):
+        copies.append([ctx.weights_from_f32((torch.randn((n, k), generator=gen, device=dev) * 0.02).contiguous())
+                       for _, n, k in shapes])
+    acts = []
+    for _ in range(args.questions):
+        per = []
+        for _, n, k in shapes:
+            x = torch.randn((M, k), generator=gen, device=dev)
+            q, s = ctx.quantize(x)
+            per.append((q, s, torch.empty((M, n), dtype=torch.float32, device=dev)))
+        acts.append(per)
+    launches = []
+    for qi in range(args.questions):
+        ws = copies[qi % len(copies)]
+        items = (dq8._Item * len(shapes))()
+        for j, (q, s, o) in enumerate(acts[qi]):
+            items[j] = dq8._Item(ws[j].handle, q.data_ptr(), s.data_ptr(), M, None, o.data_ptr(), dq8.ROWS,
+                                 dq8.WRITE)
+        launches.append(items)
+    sh = stream.cuda_stream
+
+    def go(evs=None, warm_copy=False):
+        for qi, items in enumerate(launches):
+            use = launches[0] if warm_copy else items
+            if evs is not None:
+                evs[qi][0].record(stream)
+            st = lib.dq8_linear_batch(ctx.handle, use, len(shapes), sh)
+            if st != 0:
+                raise dq8.Dq8Error(st, "dq8_linear_batch")
+            if evs is not None:
+                evs[qi][1].record(stream)
+
+    for _ in range(2):
+        go()
+    torch.cuda.synchronize()
+    reps = args.skinny_reps
+    evs = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in launches]
+           for _ in range(reps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for r in range(reps):
+        go(evs[r])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    launch_ms = sum(evs[r][i][0].elapsed_time(evs[r][i][1]) for r in range(reps) for i in range(len(launches)))
+    avg_launch = launch_ms / (reps * len(launches))
+    # MALL-resident comparison: the same launch (one weight copy) repeated
+    t0.record(stream)
+    for _ in range(reps):
+        go(warm_copy=True)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    warm_ms = t0.elapsed_time(t1)
+    gbs = wbytes * args.questions * reps / (total_ms * 1e-3) / 1e9
+    kernel_gbs = wbytes / (avg_launch * 1e-3) / 1e9
+    for ws in copies:
+        for h in ws:
+            h.free()
+    return {
+        "workload": f"{args.questions} questions x {M} tokens, one grouped launch per question over q,k,v,o,"
+                    f"GDN in/out, FFN gate/up/down ({args.weight_copies} rotating weight copies)",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "weight_bytes_per_question": wbytes,
+        "ms_per_question": round(total_ms / (reps * args.questions), 5),
+        "mall_resident_gbs": round(wbytes * args.questions * reps / (warm_ms * 1e-3) / 1e9, 1),
+        "roofline": {
+            "kernel": "k_linear_skinny",
+            "bound": "hbm",
+            "achieved": round(kernel_gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(kernel_gbs / PEAK_HBM_GBS, 4),
+            "traffic": load_traffic("linear_skinny_questions24"),
+            "bytes_per_launch": wbytes,
+            "avg_launch_ms": round(avg_launch, 5),
+        },
+    }
+
+
+def run_cpu_baseline(args, torch, dq8, ctx, dev, gen):
+    """The oracle (C restatement of the reference's x86 int8 path: per-projection
+    input quantization + per-column scalar group dots, threads over columns)
+    on the first GDN layer + its FFN for a bounded number of token rows."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import dq8o
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    rng = np.random.default_rng(5)
+    shapes = [("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN), ("gate", FFN_DIM, HIDDEN),
+              ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
+    ws = {}
+    for name, n, k in shapes:
+        h = ctx.weights_from_f32((torch.randn((n, k), generator=gen, device=dev) * 0.02).contiguous())
+        v, s = h.export()
+        torch.cuda.synchronize()
+        ws[name] = (v.cpu().numpy(), s.cpu().numpy())
+        h.free()
+
+    def layer(rows):
+        x = rng.standard_normal((rows, HIDDEN)).astype(np.float32)
+        t = time.perf_counter()
+        dq8o.linear(x, *ws["gdn_in"], threads=threads)
+        dq8o.linear(x, *ws["gdn_out"], threads=threads)
+        g = dq8o.linear(x, *ws["gate"], threads=threads)
+        g = dq8o.linear(x, *ws["up"], result=g, epilogue=2, threads=threads)
+        dq8o.linear(g, *ws["down"], result=x, epilogue=1, threads=threads)
+        return time.perf_counter() - t
+
+    ops_per_row = 2 * sum(n * k for _, n, k in shapes)
+    est = layer(2) / 2
+    rows = int(max(2, min(2048, args.cpu_seconds / max(est, 1e-6))))
+    secs = layer(rows)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(ops_per_row * rows / secs / 1e12, 5),
+        "unit": "TOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"first GDN layer + FFN projections (in 2048->8224, out, gate/up SwiGlu, re-quantized down) "
+                  f"for {rows} of the 2048 tokens, quantization included; {secs:.1f} s on {cpu_model}",
+    }
+
+
+def load_traffic(name):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic_<name>.json), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+if __name__ == "__main__":
+    main()
