@@ -75,7 +75,8 @@ dq8_status make_weights(dq8_ctx* ctx, size_t n, size_t k, dq8_weights** out) {
   h->w.values = nullptr;
   h->w.scales = nullptr;
   hipError_t e = hipMalloc(&h->w.values, (size_t)h->w.np * h->w.g * kGroup);
-  if (e == hipSuccess) e = hipMalloc(&h->w.scales, (size_t)h->w.np * h->w.g * sizeof(float));
+  // One extra all-zero row of scales: the kernels read it for groups past the end.
+  if (e == hipSuccess) e = hipMalloc(&h->w.scales, (size_t)h->w.np * (h->w.g + 1) * sizeof(float));
   if (e != hipSuccess) {
     (void)hipFree(h->w.values);
     (void)hipFree(h->w.scales);
@@ -160,8 +161,8 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     fill_proj(p, w, q, ldq, it.scales, it.m, it.bias, it.out, dots, it.layout, it.epilogue);
     p.wave_begin = b.total_waves;
     if (kind == 0) {
-      p.waves_n = w.np / 64;
-      b.total_waves += p.waves_n * (int)((it.m + 63) / 64);
+      p.waves_n = w.np / dq8::wide_block_cols();
+      b.total_waves += p.waves_n * (int)((it.m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows());
     } else {
       p.waves_n = w.np / 32;
       b.total_waves += p.waves_n;
@@ -363,8 +364,8 @@ dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, 
   fill_proj(p, w->w, q, (int)ldq, xs, m, bias, out, nullptr, layout, epilogue);
   p.wave_begin = 0;
   const int kind = m <= 32 ? 1 : 0;
-  p.waves_n = kind == 0 ? w->w.np / 64 : w->w.np / 32;
-  b.total_waves = kind == 0 ? p.waves_n * (int)((m + 63) / 64) : p.waves_n;
+  p.waves_n = kind == 0 ? w->w.np / dq8::wide_block_cols() : w->w.np / 32;
+  b.total_waves = kind == 0 ? p.waves_n * (int)((m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows()) : p.waves_n;
   return from_hip(dq8::launch_linear(b, kind, false, s));
 }
 

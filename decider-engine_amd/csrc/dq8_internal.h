@@ -10,14 +10,13 @@ namespace dq8 {
 constexpr int kGroup = 64;        // reference group width (weights.rs:119, tensor.rs:329)
 constexpr int kFragBytes = 1024;  // one MFMA operand fragment: 64 lanes x 16 bytes
 constexpr int kMaxBatch = 16;     // projections per launch
-constexpr int kWaveRows = 64;     // rows per wave in the wide kernel
-constexpr int kColPad = 64;       // weights are padded to a multiple of this many outputs
+constexpr int kColPad = 256;      // weights are padded to a multiple of this many outputs
 
 // Repacked weights, owned by a dq8_weights handle.
 //   values: [Np/32][G][2][64 lanes][16 bytes]; fragment (nb, g, h) holds, at lane l,
 //           output row nb*32 + l%32 and input bytes g*64 + 32h + 16*(l/32) .. +16
 //           (zero beyond N or K).
-//   scales: [G][Np] fp32, group-major (zero beyond N).
+//   scales: [G + 1][Np] fp32, group-major (zero beyond N; row G all zero).
 struct Weights {
   int device;
   int n, k, g, np;
@@ -38,14 +37,14 @@ struct Proj {
   int m, ldq, g, n, np;
   int epilogue;       // 0 write, 1 add, 2 swiglu
   int layout;         // 0 rows [M][N], 1 columns [N][M]
-  int wave_begin;     // first wave of this projection in the launch
-  int waves_n;        // column strips of this projection
+  int wave_begin;     // first wave (skinny) or block (wide) of this projection in the launch
+  int waves_n;        // column strips (skinny: 32 wide, wide: one block tile wide)
 };
 
 struct Batch {
   Proj p[kMaxBatch];
   int count;
-  int total_waves;
+  int total_waves;  // waves (skinny) or blocks (wide) of the launch
 };
 
 // Kernel launchers (dq8_kernels.hip).  All return hipError_t of the launch.
@@ -56,5 +55,8 @@ hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipSt
 hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ldq, hipStream_t s);
 // Kind: 0 wide (M > 32), 1 skinny (M <= 32).  dots selects the debug kernel.
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s);
+// Block tile of the wide kernel (rows, columns); kColPad is a multiple of the columns.
+int wide_block_rows();
+int wide_block_cols();
 
 }  // namespace dq8

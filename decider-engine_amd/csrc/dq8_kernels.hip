@@ -155,11 +155,12 @@ __global__ void k_repack_values(const uint8_t* __restrict__ values, int n, int k
   *reinterpret_cast<uint4*>(wt + i * 16) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
+// wst has G + 1 rows; row G is all zero (the scale of groups past the end).
 __global__ void k_repack_scales(const float* __restrict__ scales, int n, int g, int np, float* __restrict__ wst) {
   long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long)g * np) return;
+  if (i >= (long)(g + 1) * np) return;
   const int gi = (int)(i / np), col = (int)(i % np);
-  wst[i] = col < n ? scales[(size_t)col * g + gi] : 0.0f;
+  wst[i] = (col < n && gi < g) ? scales[(size_t)col * g + gi] : 0.0f;
 }
 
 __global__ void k_export_values(const uint8_t* __restrict__ wt, int n, int k, int g, uint8_t* __restrict__ values) {
@@ -187,31 +188,324 @@ __global__ void k_pad_rows(const int8_t* __restrict__ q, int rows, int k, int8_t
 }
 
 // ---------------------------------------------------------------------------
-// Wide projection kernel (M > 32).  Each wave owns a 64 x 64 output tile:
-// row tiles r0, r1 (32 rows each) x column tiles j0, j1.  Per group, for each
-// column tile j the pair (r0, j), (r1, j) shares one conversion MFMA and one
-// product MFMA: A lane l carries x scale of row m0 + l, B lane l carries the
-// w scale of column n0 + 32j + l%32.
-template <bool DOTS>
-__global__ __launch_bounds__(256) void k_linear_wide(Batch b) {
+// Wide projection kernel (M > 32), LDS-staged.  A block of WM x WN waves owns
+// a (64*WM) x (64*WN) output tile; each wave owns 64 x 64 of it: row tiles
+// r0, r1 (32 rows each) x column tiles j0, j1.  Per group, for each column
+// tile j the pair (r0, j), (r1, j) shares one conversion MFMA and one product
+// MFMA: A lane l carries the x scale of row m0 + l, B lane l the w scale of
+// column n0 + 32j + l%32.
+//
+// Operands reach LDS by direct global->LDS loads (global_load_lds_dwordx4:
+// lane l's 16 bytes land at base + 16*l, i.e. fragments stay in lane order and
+// LDS reads are conflict-free ds_read_b128).  STAGES groups are in flight in
+// an LDS ring.  Iteration g: wait for this wave's loads of group g
+// (vmcnt <= loads of the STAGES-2 newer groups), barrier (every wave's loads
+// of group g have landed and every wave is done reading group g-1), issue the
+// loads of group g+STAGES-1 into group g-1's buffer, then read group g and
+// compute.  Groups past the end load clamped operands and the all-zero w scale
+// row G, so p = 0, t = dot * 0 = +-0 and s + t = s (s is never -0).
+
+// Consecutive tiles of a projection go to the same XCD (blocks are dealt to
+// the 8 XCDs round robin), so neighbours share A rows in that XCD's L2.
+__device__ __forceinline__ int xcd_tile(int i, int tiles) {
+  if (tiles % 8 != 0) return i;
+  return (i & 7) * (tiles >> 3) + (i >> 3);
+}
+
+// Direct global->LDS loads.  They are issued through inline assembly so the
+// compiler does not track them: its LDS-DMA bookkeeping is conservative at
+// loop headers and would drain the whole pipeline there.  The kernel orders
+// every use itself (wait_vmcnt + s_barrier).  No compiler-generated code in
+// these kernels uses M0; the s_nop covers the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ void dma16(const void* src, const void* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_offset(lds)), "v"(src)
+               : "memory");
+}
+__device__ __forceinline__ void dma4(const void* src, const void* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :
+               : "s"(lds_offset(lds)), "v"(src)
+               : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Launch shape of the wide kernel (tunable at build time):
+//   WM x WN waves per block, each wave (32*RT) rows x (32*CT) columns;
+//   STAGES groups in flight in LDS; CVT_VALU converts the dots on the VALU
+//   (C = 0) instead of the K=1 MFMA (C = bias bits).
+#ifndef DQ8_WIDE_WM
+#define DQ8_WIDE_WM 2
+#endif
+#ifndef DQ8_WIDE_WN
+#define DQ8_WIDE_WN 2
+#endif
+#ifndef DQ8_WIDE_RT
+#define DQ8_WIDE_RT 1
+#endif
+#ifndef DQ8_WIDE_CT
+#define DQ8_WIDE_CT 2
+#endif
+#ifndef DQ8_WIDE_STAGES
+#define DQ8_WIDE_STAGES 4
+#endif
+#ifndef DQ8_WIDE_CVT_VALU
+#define DQ8_WIDE_CVT_VALU 0
+#endif
+
+// A wave's 32x32 tiles are processed in pairs that share one conversion and one
+// product MFMA (blocks 0 and 1 of v_mfma_f32_32x32x1_2b_f32):
+//   RT == 2: pair j = row tiles (0, 1) at column tile j;  A lane l: x of row l,
+//            B lane l: w of column 32j + l%32.
+//   RT == 1: one pair = column tiles (0, 1) at the single row tile;  A lane l:
+//            x of row l%32, B lane l: w of column l.
+template <int WM, int WN, int RT, int CT, int STAGES, bool CVT_VALU, bool DOTS>
+__global__ __launch_bounds__(64 * WM * WN) void k_linear_wide(Batch b) {
+  constexpr int NW = WM * WN, WR = 32 * RT, WC = 32 * CT;  // wave tile WR x WC
+  constexpr int BM = WR * WM, BN = WC * WN;
+  constexpr int AF = BM / 16, BF = BN / 16, NF = AF + BF;  // 1 KB fragments per group
+  constexpr int FPW = NF / NW;
+  constexpr int SCW = (BM + BN) / 64;           // waves holding real scales
+  constexpr int LOADS = FPW + (DOTS ? 0 : 1);   // DMA instructions per wave per group
+  constexpr int NP = RT == 2 ? CT : 1;          // pairs per wave
+  static_assert(NF % NW == 0, "fragments must split evenly over the waves");
+  static_assert(BM % 64 == 0 && BN % 64 == 0 && SCW <= NW, "64 scales per staging wave");
+  static_assert((RT == 2 && (CT == 1 || CT == 2)) || (RT == 1 && CT == 2), "supported wave tiles");
+  static_assert(STAGES >= 2 && STAGES <= 4 && LOADS * (STAGES - 2) <= 63, "pipeline depth");
+  // One LDS object per stage, always indexed by compile-time constants.
+  struct Stage {
+    uint8_t frag[NF][kFragBytes];
+    float sc[64 * NW];  // x scales of the BM rows, w scales of the BN columns, then padding
+  };
+  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2, st3;
+  auto stage = [&](int i) -> Stage& { return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3; };
+
   const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (wave >= b.total_waves) return;
-  const Proj& P = b.p[find_proj(b, wave)];
-  const int w = wave - P.wave_begin;
-  const int mt = w / P.waves_n, nt = w - mt * P.waves_n;
-  const int m0 = mt * 64, n0 = nt * 64;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
+  const int blk = blockIdx.x;
+  const Proj& P = b.p[find_proj(b, blk)];
+  const int tiles = P.waves_n * ((P.m + BM - 1) / BM);
+  const int t = xcd_tile(blk - P.wave_begin, tiles);
+  const int mt = t / P.waves_n, nt = t - mt * P.waves_n;
+  const int m0 = mt * BM, n0 = nt * BN;
   const int G = P.g;
 
-  const int r_lo = min(m0 + (lane & 31), P.m - 1);
-  const int r_hi = min(m0 + 32 + (lane & 31), P.m - 1);
-  const int8_t* pa0 = P.q + (size_t)r_lo * P.ldq + 16 * (lane >> 5);
-  const int8_t* pa1 = P.q + (size_t)r_hi * P.ldq + 16 * (lane >> 5);
-  const uint8_t* pb0 = P.wt + (size_t)(n0 / 32) * G * 2 * kFragBytes + lane * 16;
-  const uint8_t* pb1 = pb0 + (size_t)G * 2 * kFragBytes;
-  const float* pxs = P.xs + (size_t)min(m0 + lane, P.m - 1) * G;
-  const float* pws0 = P.wst + n0 + (lane & 31);
-  const float* pws1 = pws0 + 32;
+  // Global sources of this wave's fragments: A (row tile, half) or B (column tile, half).
+  const uint8_t* src[FPW];
+  int stride[FPW];
+#pragma unroll
+  for (int i = 0; i < FPW; ++i) {
+    const int f = wid + i * NW;
+    if (f < AF) {
+      const int row = min(m0 + 32 * (f >> 1) + (lane & 31), P.m - 1);
+      src[i] = reinterpret_cast<const uint8_t*>(P.q) + (size_t)row * P.ldq + 32 * (f & 1) + 16 * (lane >> 5);
+      stride[i] = kGroup;
+    } else {
+      const int fb = f - AF;
+      src[i] = P.wt + ((size_t)(n0 / 32 + (fb >> 1)) * G * 2 + (fb & 1)) * kFragBytes + lane * 16;
+      stride[i] = 2 * kFragBytes;
+    }
+  }
+  // Scales: the first BM/64 waves stage x scales of 64 rows each, the next BN/64
+  // waves w scales of 64 columns; the rest load a harmless duplicate into the
+  // padding so that every wave issues the same number of loads.  x scales clamp
+  // to the last group, w scales run into the zero row G.
+  const int sw = wid < SCW ? wid : 0;
+  const bool xwave = sw < BM / 64;
+  const float* psc = xwave ? P.xs + (size_t)min(m0 + 64 * sw + lane, P.m - 1) * G
+                           : P.wst + n0 + 64 * (sw - BM / 64) + lane;
+  const size_t sstride = xwave ? 1 : (size_t)P.np;
+  const int slast = xwave ? G - 1 : G;
+
+  auto issue = [&](Stage& S, int g) {
+    const int gc = min(g, G - 1);
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) dma16(src[i] + (size_t)gc * stride[i], &S.frag[wid + i * NW][0]);
+    if constexpr (!DOTS) dma4(psc + (size_t)min(g, slast) * sstride, &S.sc[64 * wid]);
+  };
+
+  const int wm = wid / WN, wn = wid - (wid / WN) * WN;
+  const int fa = 2 * RT * wm;   // first A fragment of this wave
+  const int fbw = AF + 2 * CT * wn;  // first B fragment
+
+  v16i cinit;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) cinit[i] = CVT_VALU ? 0 : kMagicBits;
+  v32f zero32;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) zero32[i] = 0.0f;
+  v32f s[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) s[j] = zero32;
+
+#pragma unroll
+  for (int i = 0; i < STAGES - 1; ++i) {
+    issue(stage(i), i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int g0 = 0; g0 < G; g0 += STAGES) {
+#pragma unroll
+    for (int d = 0; d < STAGES; ++d) {
+      const int g = g0 + d;
+      if (g >= G) break;  // uniform over the block
+      Stage& cur = stage(d);
+      wait_vmcnt<LOADS * (STAGES - 2)>();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(stage((d + STAGES - 1) % STAGES), g + STAGES - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      const v4i* fr = reinterpret_cast<const v4i*>(&cur.frag[0][0]);
+      v4i af[RT][2], bf[CT][2];
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        af[r][0] = fr[(fa + 2 * r) * 64 + lane];
+        af[r][1] = fr[(fa + 2 * r + 1) * 64 + lane];
+      }
+#pragma unroll
+      for (int j = 0; j < CT; ++j) {
+        bf[j][0] = fr[(fbw + 2 * j) * 64 + lane];
+        bf[j][1] = fr[(fbw + 2 * j + 1) * 64 + lane];
+      }
+      // dt[r][j]: dot tile of row tile r, column tile j (two MFMAs, K = 32 each).
+      v16i dt[RT][CT];
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int j = 0; j < CT; ++j) dt[r][j] = mfma_i8(af[r][0], bf[j][0], cinit);
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int j = 0; j < CT; ++j) dt[r][j] = mfma_i8(af[r][1], bf[j][1], dt[r][j]);
+      if constexpr (DOTS) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+          for (int j = 0; j < CT; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int row = m0 + WR * wm + 32 * r + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+              const int col = n0 + WC * wn + 32 * j + (lane & 31);
+              if (row < P.m && col < P.n)
+                P.dots[((size_t)row * P.n + col) * G + g] = dt[r][j][v] - (CVT_VALU ? 0 : kMagicBits);
+            }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+          const v16i& lo = RT == 2 ? dt[0][j] : dt[0][0];
+          const v16i& hi = RT == 2 ? dt[1][j] : dt[0][1];
+          float x, w;
+          if constexpr (RT == 2) {
+            x = cur.sc[WR * wm + lane];
+            w = cur.sc[BM + WC * wn + 32 * j + (lane & 31)];
+          } else {
+            x = cur.sc[WR * wm + (lane & 31)];
+            w = cur.sc[BM + WC * wn + lane];
+          }
+          v32f dv;
+          if constexpr (CVT_VALU) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              dv[v] = (float)lo[v];
+              dv[16 + v] = (float)hi[v];
+            }
+          } else {
+            dv = mfma_k1(-kMagic, 1.0f, concat(lo, hi));
+          }
+          const v32f pv = mfma_k1(x, w, zero32);
+          s[j] = s[j] + dv * pv;
+        }
+      }
+    }
+  }
+  // Drain the clamped loads of the groups past the end before the block exits.
+  wait_vmcnt<0>();
+  if constexpr (!DOTS) {
+    const int mw = m0 + WR * wm, nw = n0 + WC * wn;
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+      for (int v = 0; v < 32; ++v) {
+        const int blk2 = v >> 4, vv = v & 15;
+        const int r = RT == 2 ? blk2 : 0, c = RT == 2 ? j : blk2;
+        const int row = mw + 32 * r + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);
+        const int col = nw + 32 * c + (lane & 31);
+        if (row < P.m && col < P.n) store_out(P, row, col, s[j][v] + (P.bias ? P.bias[col] : 0.0f));
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Software-pipelined wide kernel.  Same data path as k_linear_wide with a
+// 32 x 64 wave tile (one row tile, column tiles c0 and c1 paired in the K=1
+// MFMAs), but the i8 MFMAs of group g+1 are issued before the conversion,
+// product and VALU work of group g, so the dependency latency of one group is
+// covered by the independent MFMAs of the next.  Stage buffers: group g's
+// fragments are read one iteration before its scales; the DMA issued in
+// iteration g refills the buffer of group g-1, which no wave reads any more.
+template <int WM, int WN, int STAGES>
+__global__ __launch_bounds__(64 * WM * WN) void k_linear_wide_sp(Batch b) {
+  constexpr int NW = WM * WN, BM = 32 * WM, BN = 64 * WN;
+  constexpr int AF = BM / 16, BF = BN / 16, NF = AF + BF;
+  constexpr int FPW = NF / NW;
+  constexpr int SCW = (BM + BN) / 64;
+  constexpr int LOADS = FPW + 1;
+  static_assert(NF % NW == 0, "fragments must split evenly over the waves");
+  static_assert(BM % 64 == 0 && BN % 64 == 0 && SCW <= NW, "64 scales per staging wave");
+  static_assert(STAGES >= 3 && STAGES <= 4 && LOADS * (STAGES - 3) <= 63, "pipeline depth");
+  struct Stage {
+    uint8_t frag[NF][kFragBytes];
+    float sc[64 * NW];
+  };
+  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2, st3;
+  auto stage = [&](int i) -> Stage& { return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3; };
+
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const Proj& P = b.p[find_proj(b, blockIdx.x)];
+  const int tiles = P.waves_n * ((P.m + BM - 1) / BM);
+  const int t = xcd_tile(blockIdx.x - P.wave_begin, tiles);
+  const int mt = t / P.waves_n, nt = t - mt * P.waves_n;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int G = P.g;
+
+  const uint8_t* src[FPW];
+  int stride[FPW];
+#pragma unroll
+  for (int i = 0; i < FPW; ++i) {
+    const int f = wid + i * NW;
+    if (f < AF) {
+      const int row = min(m0 + 32 * (f >> 1) + (lane & 31), P.m - 1);
+      src[i] = reinterpret_cast<const uint8_t*>(P.q) + (size_t)row * P.ldq + 32 * (f & 1) + 16 * (lane >> 5);
+      stride[i] = kGroup;
+    } else {
+      const int fb = f - AF;
+      src[i] = P.wt + ((size_t)(n0 / 32 + (fb >> 1)) * G * 2 + (fb & 1)) * kFragBytes + lane * 16;
+      stride[i] = 2 * kFragBytes;
+    }
+  }
+  const int sw = wid < SCW ? wid : 0;
+  const bool xwave = sw < BM / 64;
+  const float* psc = xwave ? P.xs + (size_t)min(m0 + 64 * sw + lane, P.m - 1) * G
+                           : P.wst + n0 + 64 * (sw - BM / 64) + lane;
+  const size_t sstride = xwave ? 1 : (size_t)P.np;
+  const int slast = xwave ? G - 1 : G;
+  auto issue = [&](Stage& S, int g) {
+    const int gc = min(g, G - 1);
+#pragma unroll
+    for (int i = 0; i < FPW; ++i) dma16(src[i] + (size_t)gc * stride[i], &S.frag[wid + i * NW][0]);
+    dma4(psc + (size_t)min(g, slast) * sstride, &S.sc[64 * wid]);
+  };
+
+  const int wm = wid / WN, wn = wid - (wid / WN) * WN;
+  const int fa = 2 * wm, fbw = AF + 4 * wn;
 
   v16i magic;
 #pragma unroll
@@ -219,83 +513,83 @@ __global__ __launch_bounds__(256) void k_linear_wide(Batch b) {
   v32f zero32;
 #pragma unroll
   for (int i = 0; i < 32; ++i) zero32[i] = 0.0f;
-  v32f s0 = zero32, s1 = zero32;
+  v32f s = zero32;
 
-  v4i a00 = load16(pa0), a01 = load16(pa0 + 32), a10 = load16(pa1), a11 = load16(pa1 + 32);
-  v4i b00 = load16(pb0), b01 = load16(pb0 + kFragBytes), b10 = load16(pb1), b11 = load16(pb1 + kFragBytes);
-  // The dots kernels read no scales (their xs may be a placeholder).
-  float xv = DOTS ? 0.0f : pxs[0], wv0 = DOTS ? 0.0f : pws0[0], wv1 = DOTS ? 0.0f : pws1[0];
+  auto dots = [&](Stage& S, v16i& d0, v16i& d1) {
+    const v4i* fr = reinterpret_cast<const v4i*>(&S.frag[0][0]);
+    const v4i a0 = fr[(fa + 0) * 64 + lane], a1 = fr[(fa + 1) * 64 + lane];
+    const v4i b0 = fr[(fbw + 0) * 64 + lane], b1 = fr[(fbw + 1) * 64 + lane];
+    const v4i b2 = fr[(fbw + 2) * 64 + lane], b3 = fr[(fbw + 3) * 64 + lane];
+    d0 = mfma_i8(a0, b0, magic);
+    d1 = mfma_i8(a0, b2, magic);
+    d0 = mfma_i8(a1, b1, d0);
+    d1 = mfma_i8(a1, b3, d1);
+  };
+  auto finish = [&](Stage& S, const v16i& d0, const v16i& d1) {
+    const float x = S.sc[32 * wm + (lane & 31)];
+    const float w = S.sc[BM + 64 * wn + lane];
+    const v32f dv = mfma_k1(-kMagic, 1.0f, concat(d0, d1));
+    const v32f pv = mfma_k1(x, w, zero32);
+    s = s + dv * pv;
+  };
 
-  for (int g = 0; g < G; ++g) {
-    const v4i ca00 = a00, ca01 = a01, ca10 = a10, ca11 = a11;
-    const v4i cb00 = b00, cb01 = b01, cb10 = b10, cb11 = b11;
-    const float cx = xv, cw0 = wv0, cw1 = wv1;
-    if (g + 1 < G) {
-      const int ao = (g + 1) * kGroup;
-      const size_t bo = (size_t)(g + 1) * 2 * kFragBytes;
-      a00 = load16(pa0 + ao); a01 = load16(pa0 + ao + 32);
-      a10 = load16(pa1 + ao); a11 = load16(pa1 + ao + 32);
-      b00 = load16(pb0 + bo); b01 = load16(pb0 + bo + kFragBytes);
-      b10 = load16(pb1 + bo); b11 = load16(pb1 + bo + kFragBytes);
-      if constexpr (!DOTS) {
-        xv = pxs[g + 1];
-        wv0 = pws0[(size_t)(g + 1) * P.np];
-        wv1 = pws1[(size_t)(g + 1) * P.np];
-      }
-    }
-    v16i d00 = mfma_i8(ca00, cb00, magic);
-    d00 = mfma_i8(ca01, cb01, d00);
-    v16i d10 = mfma_i8(ca10, cb00, magic);
-    d10 = mfma_i8(ca11, cb01, d10);
-    v16i d01 = mfma_i8(ca00, cb10, magic);
-    d01 = mfma_i8(ca01, cb11, d01);
-    v16i d11 = mfma_i8(ca10, cb10, magic);
-    d11 = mfma_i8(ca11, cb11, d11);
-    if constexpr (DOTS) {
-      // dots[(row * N + col) * G + g] = dot_g for the four 32x32 tiles
+  // Prologue: stages 0 .. STAGES-2 in flight; dots of group 0.
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const v16i& d = t == 0 ? d00 : t == 1 ? d10 : t == 2 ? d01 : d11;
-        const int rt = t & 1, ct = t >> 1;
+  for (int i = 0; i < STAGES - 1; ++i) {
+    issue(stage(i), i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_vmcnt<LOADS * (STAGES - 2)>();
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  v16i c0, c1;
+  dots(stage(0), c0, c1);
+  for (int g0 = 0; g0 < G; g0 += STAGES) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = m0 + 32 * rt + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-          const int col = n0 + 32 * ct + (lane & 31);
-          if (row < P.m && col < P.n) P.dots[((size_t)row * P.n + col) * G + g] = d[v] - kMagicBits;
-        }
-      }
-    } else {
-      const v32f dv0 = mfma_k1(-kMagic, 1.0f, concat(d00, d10));
-      const v32f pv0 = mfma_k1(cx, cw0, zero32);
-      const v32f dv1 = mfma_k1(-kMagic, 1.0f, concat(d01, d11));
-      const v32f pv1 = mfma_k1(cx, cw1, zero32);
-      s0 = s0 + dv0 * pv0;
-      s1 = s1 + dv1 * pv1;
+    for (int d = 0; d < STAGES; ++d) {
+      const int g = g0 + d;
+      if (g >= G) break;  // uniform over the block
+      // Group g+1 has landed everywhere; every wave is done with group g-1.
+      wait_vmcnt<LOADS * (STAGES - 3)>();
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(stage((d + STAGES - 1) % STAGES), g + STAGES - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      v16i n0_, n1_;
+      dots(stage((d + 1) % STAGES), n0_, n1_);  // group g+1 (clamped data past the end is unused)
+      finish(stage(d), c0, c1);
+      c0 = n0_;
+      c1 = n1_;
     }
   }
-  if constexpr (!DOTS) {
+  wait_vmcnt<0>();
+  const int mw = m0 + 32 * wm, nw = n0 + 64 * wn;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const v32f& s = j == 0 ? s0 : s1;
-      const int col = n0 + 32 * j + (lane & 31);
-      if (col >= P.n) continue;
-      const float bias = P.bias ? P.bias[col] : 0.0f;
-#pragma unroll
-      for (int v = 0; v < 32; ++v) {
-        const int vv = v & 15;
-        const int row = m0 + 32 * (v >> 4) + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);
-        if (row < P.m) store_out(P, row, col, s[v] + bias);
-      }
-    }
+  for (int v = 0; v < 32; ++v) {
+    const int blk2 = v >> 4, vv = v & 15;
+    const int row = mw + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);
+    const int col = nw + 32 * blk2 + (lane & 31);
+    if (row < P.m && col < P.n) store_out(P, row, col, s[v] + (P.bias ? P.bias[col] : 0.0f));
   }
 }
 
 // ---------------------------------------------------------------------------
 // Skinny projection kernel (M <= 32): weight-streaming.  Each wave owns all
-// (padded) 32 rows x one 32-column tile and walks the groups two at a time;
-// the K=1 MFMAs pair group g (block 0) with group g+1 (block 1), and the fp32
-// sum adds group g's terms before group g+1's.
-template <bool DOTS>
+// (padded) 32 rows x one 32-column tile and walks the groups two at a time
+// (a "step"); the K=1 MFMAs pair group g (block 0) with group g+1 (block 1),
+// and the fp32 sum adds group g's terms before group g+1's.  DEPTH steps of
+// operands are in flight (weights stream from HBM; activations are L2-hot).
+// Groups past the end read clamped operands and the zero w scale row G.
+// This kernel is bandwidth-bound, so the dots start from C = 0 and convert on
+// the VALU (exact: |dot| <= 2^20), which frees the 16 registers of the bias
+// constant for the prefetch ring.
+struct SkinnyFrag {
+  v4i a[4];  // (g,h0) (g,h1) (g+1,h0) (g+1,h1)
+  v4i b[4];
+  float x, w;
+};
+
+template <int DEPTH, bool DOTS>
 __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -305,6 +599,7 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   const int n0 = nt * 32;
   const int G = P.g;
   const int half = lane >> 5;
+  const int steps = (G + 1) >> 1;
 
   const int row = min(lane & 31, P.m - 1);
   const int8_t* pa = P.q + (size_t)row * P.ldq + 16 * half;
@@ -312,9 +607,25 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   const float* pxs = P.xs + (size_t)row * G;
   const float* pws = P.wst + n0 + (lane & 31);
 
-  v16i magic;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) magic[i] = kMagicBits;
+  auto load = [&](SkinnyFrag& f, int step) {
+    const int g = 2 * step;
+    const int ga = min(g, G - 1), gb = min(g + 1, G - 1);
+    f.a[0] = load16(pa + ga * kGroup);
+    f.a[1] = load16(pa + ga * kGroup + 32);
+    f.a[2] = load16(pa + gb * kGroup);
+    f.a[3] = load16(pa + gb * kGroup + 32);
+    f.b[0] = load16(pb + (size_t)ga * 2 * kFragBytes);
+    f.b[1] = load16(pb + (size_t)(ga * 2 + 1) * kFragBytes);
+    f.b[2] = load16(pb + (size_t)gb * 2 * kFragBytes);
+    f.b[3] = load16(pb + (size_t)(gb * 2 + 1) * kFragBytes);
+    if constexpr (!DOTS) {
+      const int gl = g + half;  // group carried by this lane's half of the K=1 operands
+      f.x = pxs[min(gl, G - 1)];
+      f.w = pws[(size_t)min(gl, G) * P.np];  // row G of the w scales is zero
+    }
+  };
+
+  const v16i zero16 = {};
   v32f zero32;
 #pragma unroll
   for (int i = 0; i < 32; ++i) zero32[i] = 0.0f;
@@ -322,43 +633,54 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) s[i] = 0.0f;
 
-  const v4i z4 = {0, 0, 0, 0};
-  for (int g = 0; g < G; g += 2) {
-    const bool two = g + 1 < G;
-    const v4i a00 = load16(pa + g * kGroup), a01 = load16(pa + g * kGroup + 32);
-    const v4i b00 = load16(pb + (size_t)g * 2 * kFragBytes), b01 = load16(pb + (size_t)(g * 2 + 1) * kFragBytes);
-    v4i a10 = z4, a11 = z4, b10 = z4, b11 = z4;
-    if (two) {
-      a10 = load16(pa + (g + 1) * kGroup); a11 = load16(pa + (g + 1) * kGroup + 32);
-      b10 = load16(pb + (size_t)(g + 1) * 2 * kFragBytes);
-      b11 = load16(pb + (size_t)((g + 1) * 2 + 1) * kFragBytes);
-    }
-    const int gl = g + half;  // group carried by this lane's half of the K=1 operands
-    const float xv = (!DOTS && gl < G) ? pxs[gl] : 0.0f;
-    const float wv = (!DOTS && gl < G) ? pws[(size_t)gl * P.np] : 0.0f;
-
-    v16i d0 = mfma_i8(a00, b00, magic);
-    d0 = mfma_i8(a01, b01, d0);
-    v16i d1 = mfma_i8(a10, b10, magic);
-    d1 = mfma_i8(a11, b11, d1);
-    if constexpr (DOTS) {
+  SkinnyFrag ring[DEPTH];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (t == 1 && !two) break;
-        const v16i& d = t == 0 ? d0 : d1;
+  for (int d = 0; d < DEPTH; ++d) {
+    // Issue the prologue in ring order so the loop's wait counts hold on entry too.
+    load(ring[d], d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  for (int s0 = 0; s0 < steps; s0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int step = s0 + d;
+      const SkinnyFrag& c = ring[d];
+      v16i d0 = mfma_i8(c.a[0], c.b[0], zero16);
+      v16i d1 = mfma_i8(c.a[2], c.b[2], zero16);
+      d0 = mfma_i8(c.a[1], c.b[1], d0);
+      d1 = mfma_i8(c.a[3], c.b[3], d1);
+      v32f pv;
+      if constexpr (!DOTS) pv = mfma_k1(c.x, c.w, zero32);
+      // Refill the slot once every operand of it is consumed: the loads reuse
+      // the slot's registers (no loop-carried copies) and have DEPTH - 1 steps to land.
+      __builtin_amdgcn_sched_barrier(0);
+      load(ring[d], step + DEPTH);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (DOTS) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int g = 2 * step + t;
+          if (g >= G) break;
+          const v16i& dd = t == 0 ? d0 : d1;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int r = 8 * (v >> 2) + 4 * half + (v & 3);
+            const int col = n0 + (lane & 31);
+            if (r < P.m && col < P.n) P.dots[((size_t)r * P.n + col) * G + g] = dd[v];
+          }
+        }
+      } else {
+        v32f dv;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int r = 8 * (v >> 2) + 4 * half + (v & 3);
-          const int col = n0 + (lane & 31);
-          if (r < P.m && col < P.n) P.dots[((size_t)r * P.n + col) * G + g + t] = d[v] - kMagicBits;
+          dv[v] = (float)d0[v];
+          dv[16 + v] = (float)d1[v];
         }
+        const v32f t = dv * pv;
+        s = s + __builtin_shufflevector(t, t, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+        s = s + __builtin_shufflevector(t, t, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31);
       }
-    } else {
-      const v32f dv = mfma_k1(-kMagic, 1.0f, concat(d0, d1));
-      const v32f pv = mfma_k1(xv, wv, zero32);
-      const v32f t = dv * pv;
-      s = s + __builtin_shufflevector(t, t, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
-      s = s + __builtin_shufflevector(t, t, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31);
     }
   }
   if constexpr (!DOTS) {
@@ -391,7 +713,7 @@ hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int 
   k_repack_values<<<blocks_for(chunks, 256), 256, 0, s>>>(values, n, k, w->g, w->values, chunks);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  k_repack_scales<<<blocks_for((long)w->g * w->np, 256), 256, 0, s>>>(scales, n, w->g, w->np, w->scales);
+  k_repack_scales<<<blocks_for((long)(w->g + 1) * w->np, 256), 256, 0, s>>>(scales, n, w->g, w->np, w->scales);
   return hipGetLastError();
 }
 
@@ -408,15 +730,33 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
   return hipGetLastError();
 }
 
+#ifndef DQ8_WIDE_SP
+#define DQ8_WIDE_SP 0
+#endif
+int wide_block_rows() { return DQ8_WIDE_SP ? 32 * DQ8_WIDE_WM : 32 * DQ8_WIDE_RT * DQ8_WIDE_WM; }
+int wide_block_cols() { return DQ8_WIDE_SP ? 64 * DQ8_WIDE_WN : 32 * DQ8_WIDE_CT * DQ8_WIDE_WN; }
+
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
   if (b.total_waves == 0) return hipSuccess;
-  const unsigned blocks = blocks_for(b.total_waves, 4);
   if (kind == 0) {
-    if (dots) k_linear_wide<true><<<blocks, 256, 0, s>>>(b);
-    else k_linear_wide<false><<<blocks, 256, 0, s>>>(b);
-  } else {
-    if (dots) k_linear_skinny<true><<<blocks, 256, 0, s>>>(b);
-    else k_linear_skinny<false><<<blocks, 256, 0, s>>>(b);
+    // total_waves counts blocks for the wide kernel
+    constexpr int threads = 64 * DQ8_WIDE_WM * DQ8_WIDE_WN;
+    if (DQ8_WIDE_SP && !dots) {
+      k_linear_wide_sp<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_STAGES><<<b.total_waves, threads, 0, s>>>(b);
+      return hipGetLastError();
+    }
+    if (dots)
+      k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_CVT_VALU, true>
+          <<<b.total_waves, threads, 0, s>>>(b);
+    else
+      k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_CVT_VALU, false>
+          <<<b.total_waves, threads, 0, s>>>(b);
+    return hipGetLastError();
+  }
+  const unsigned blocks = blocks_for(b.total_waves, 4);
+  {
+    if (dots) k_linear_skinny<4, true><<<blocks, 256, 0, s>>>(b);
+    else k_linear_skinny<4, false><<<blocks, 256, 0, s>>>(b);
   }
   return hipGetLastError();
 }
