@@ -131,15 +131,14 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     dq8_status st = ensure_work(ctx, need);
     if (st != DQ8_OK) return st;
   }
-  dq8::Batch batch[2];
-  batch[0].count = batch[1].count = 0;
-  batch[0].total_waves = batch[1].total_waves = 0;
+  dq8::Batch batch[3];
+  for (dq8::Batch& b : batch) b.count = b.total_waves = 0;
   size_t offset = 0;
   for (size_t i = 0; i < count; ++i) {
     const dq8_linear_item& it = items[i];
     if (it.m == 0) continue;
     const dq8::Weights& w = it.w->w;
-    const int kind = it.m <= 32 ? 1 : 0;
+    const int kind = it.m > 32 ? 0 : it.m <= 16 ? 1 : 2;
     dq8::Batch& b = batch[kind];
     if (b.count == dq8::kMaxBatch) {
       hipError_t e = dq8::launch_linear(b, kind, dots != nullptr, s);
@@ -164,11 +163,11 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
       p.waves_n = w.np / dq8::wide_block_cols();
       b.total_waves += p.waves_n * (int)((it.m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows());
     } else {
-      p.waves_n = w.np / 32;
-      b.total_waves += p.waves_n;
+      p.waves_n = w.np / dq8::skinny_cols();
+      b.total_waves += p.waves_n * dq8::skinny_row_waves((int)it.m);
     }
   }
-  for (int kind = 0; kind < 2; ++kind) {
+  for (int kind = 0; kind < 3; ++kind) {
     if (batch[kind].count == 0) continue;
     hipError_t e = dq8::launch_linear(batch[kind], kind, dots != nullptr, s);
     if (e != hipSuccess) return from_hip(e);
@@ -363,9 +362,10 @@ dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, 
   dq8::Proj& p = b.p[0];
   fill_proj(p, w->w, q, (int)ldq, xs, m, bias, out, nullptr, layout, epilogue);
   p.wave_begin = 0;
-  const int kind = m <= 32 ? 1 : 0;
-  p.waves_n = kind == 0 ? w->w.np / dq8::wide_block_cols() : w->w.np / 32;
-  b.total_waves = kind == 0 ? p.waves_n * (int)((m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows()) : p.waves_n;
+  const int kind = m > 32 ? 0 : m <= 16 ? 1 : 2;
+  p.waves_n = kind == 0 ? w->w.np / dq8::wide_block_cols() : w->w.np / dq8::skinny_cols();
+  b.total_waves = kind == 0 ? p.waves_n * (int)((m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows())
+                            : p.waves_n * dq8::skinny_row_waves((int)m);
   return from_hip(dq8::launch_linear(b, kind, false, s));
 }
 

@@ -53,8 +53,12 @@ hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, 
 hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int k, Weights* w, hipStream_t s);
 hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipStream_t s);
 hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ldq, hipStream_t s);
-// Kind: 0 wide (M > 32), 1 skinny (M <= 32).  dots selects the debug kernel.
+// Kind: 0 wide (M > 32), 1 skinny with M <= 16, 2 skinny with 16 < M <= 32.
+// dots selects the debug kernel.
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s);
+// Columns per wave of the skinny kernel, and its waves per column strip for m rows.
+int skinny_cols();
+int skinny_row_waves(int m);
 // Block tile of the wide kernel (rows, columns); kColPad is a multiple of the columns.
 int wide_block_rows();
 int wide_block_cols();

@@ -31,6 +31,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kMagicBits = 0x4B400000;
 constexpr float kMagic = 12582912.0f;
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, i
                                                   int ldq, float* __restrict__ scales, uint32_t* nonfinite) {
   const int lane = threadIdx.x & 63;
   const int chunks = (k + 255) >> 8;
-  const long item = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const long item = (long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   if (item >= (long)rows * chunks) return;
   const int row = (int)(item / chunks);
   const int chunk = (int)(item - (long)row * chunks);
@@ -592,7 +593,8 @@ struct SkinnyFrag {
 template <int DEPTH, bool DOTS>
 __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // Wave-uniform (scalar) so the projection record, G and the loop are uniform.
+  const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wave >= b.total_waves) return;
   const Proj& P = b.p[find_proj(b, wave)];
   const int nt = wave - P.wave_begin;
@@ -696,6 +698,111 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Skinny projection kernel, 16 x 16 wave tiles (M <= 32).  Each wave owns one
+// 16-row tile x 16 columns and walks the groups one at a time:
+//   v_mfma_i32_16x16x64_i8 gives one group's dots for the tile (row
+//   4*(l/16) + v, column l%16), C = the bias bits 0x4B400000;
+//   v_mfma_f32_4x4x1_16b_f32 with A = -12582912, B = 1 converts them exactly;
+//   the same instruction with A lane a = x of row 4*(a/16) + a%4 and B lane l =
+//   w of column l%16 is the product outer product in the same layout.
+// The row tiles of one 16-column strip are adjacent waves of a block, so the
+// strip's weights come from HBM once and from L1/L2 for the other row tiles.
+// Short dependency chains and many waves hide the memory latency.
+struct Skinny16Frag {
+  v4i a, b;
+  float x, w;
+};
+
+__device__ __forceinline__ v4i mfma_i8_16(v4i a, v4i b, v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ v4f mfma_k1_4(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+}
+
+template <int DEPTH, bool DOTS>
+__global__ __launch_bounds__(256) void k_linear_skinny16(Batch b) {
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (wave >= b.total_waves) return;
+  const Proj& P = b.p[find_proj(b, wave)];
+  const int rtiles = (P.m + 15) >> 4;
+  const int w_local = wave - P.wave_begin;
+  const int nt = w_local / rtiles;  // 16-column strip
+  const int r0 = (w_local - nt * rtiles) * 16;
+  const int c0 = nt * 16;
+  const int G = P.g;
+
+  // A: lane l holds row r0 + l%16, bytes 16*(l/16) of the group.
+  const int8_t* pa = P.q + (size_t)min(r0 + (lane & 15), P.m - 1) * P.ldq + 16 * (lane >> 4);
+  const float* pxs = P.xs + (size_t)min(r0 + 4 * (lane >> 4) + (lane & 3), P.m - 1) * G;  // K=1 A-lane row
+  // B: lane l holds column c0 + l%16, bytes 16*(l/16): in the 32-row fragment
+  // layout that is half l/32, lane (c0%32) + l%16 + 32*((l/16)&1).
+  const uint8_t* pb = P.wt + ((size_t)(c0 / 32) * G * 2 + (lane >> 5)) * kFragBytes +
+                      ((c0 & 31) + (lane & 15) + 32 * ((lane >> 4) & 1)) * 16;
+  const float* pws = P.wst + c0 + (lane & 15);
+
+  auto load = [&](Skinny16Frag& f, int g) {
+    const int gc = min(g, G - 1);
+    f.a = load16(pa + gc * kGroup);
+    f.b = load16(pb + (size_t)gc * 2 * kFragBytes);
+    if constexpr (!DOTS) {
+      f.x = pxs[gc];
+      f.w = pws[(size_t)min(g, G) * P.np];  // row G of the w scales is zero
+    }
+  };
+
+  v4i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+  const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  v4f s = zero4;
+
+  Skinny16Frag ring[DEPTH];
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    load(ring[d], d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int g0 = 0; g0 < G; g0 += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int g = g0 + d;
+      const Skinny16Frag& c = ring[d];
+      const v4i dd = mfma_i8_16(c.a, c.b, magic);
+      v4f pv;
+      if constexpr (!DOTS) pv = mfma_k1_4(c.x, c.w, zero4);
+      // Refill the slot once every operand of it is consumed.
+      __builtin_amdgcn_sched_barrier(0);
+      load(ring[d], g + DEPTH);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (DOTS) {
+        if (g < G) {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int row = r0 + 4 * (lane >> 4) + v;
+            const int col = c0 + (lane & 15);
+            if (row < P.m && col < P.n) P.dots[((size_t)row * P.n + col) * G + g] = dd[v] - kMagicBits;
+          }
+        }
+      } else {
+        const v4f dv = mfma_k1_4(-kMagic, 1.0f, __builtin_bit_cast(v4f, dd));
+        s = s + dv * pv;
+      }
+    }
+  }
+  if constexpr (!DOTS) {
+    const int col = c0 + (lane & 15);
+    if (col < P.n) {
+      const float bias = P.bias ? P.bias[col] : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = r0 + 4 * (lane >> 4) + v;
+        if (row < P.m) store_out(P, row, col, s[v] + bias);
+      }
+    }
+  }
+}
+
 }  // namespace
 
 static unsigned blocks_for(long n, int per) { return (unsigned)((n + per - 1) / per); }
@@ -733,6 +840,17 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
 #ifndef DQ8_WIDE_SP
 #define DQ8_WIDE_SP 0
 #endif
+#ifndef DQ8_SKINNY_DEPTH
+#define DQ8_SKINNY_DEPTH 4
+#endif
+#ifndef DQ8_SKINNY16
+#define DQ8_SKINNY16 1
+#endif
+#ifndef DQ8_SKINNY16_DEPTH
+#define DQ8_SKINNY16_DEPTH 4
+#endif
+int skinny_cols() { return DQ8_SKINNY16 ? 16 : 32; }
+int skinny_row_waves(int m) { return DQ8_SKINNY16 ? (m + 15) / 16 : 1; }
 int wide_block_rows() { return DQ8_WIDE_SP ? 32 * DQ8_WIDE_WM : 32 * DQ8_WIDE_RT * DQ8_WIDE_WM; }
 int wide_block_cols() { return DQ8_WIDE_SP ? 64 * DQ8_WIDE_WN : 32 * DQ8_WIDE_CT * DQ8_WIDE_WN; }
 
@@ -754,9 +872,14 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
     return hipGetLastError();
   }
   const unsigned blocks = blocks_for(b.total_waves, 4);
+  if (DQ8_SKINNY16) {
+    if (dots) k_linear_skinny16<DQ8_SKINNY16_DEPTH, true><<<blocks, 256, 0, s>>>(b);
+    else k_linear_skinny16<DQ8_SKINNY16_DEPTH, false><<<blocks, 256, 0, s>>>(b);
+    return hipGetLastError();
+  }
   {
-    if (dots) k_linear_skinny<4, true><<<blocks, 256, 0, s>>>(b);
-    else k_linear_skinny<4, false><<<blocks, 256, 0, s>>>(b);
+    if (dots) k_linear_skinny<DQ8_SKINNY_DEPTH, true><<<blocks, 256, 0, s>>>(b);
+    else k_linear_skinny<DQ8_SKINNY_DEPTH, false><<<blocks, 256, 0, s>>>(b);
   }
   return hipGetLastError();
 }
