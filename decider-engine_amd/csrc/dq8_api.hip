@@ -106,6 +106,42 @@ void fill_proj(dq8::Proj& p, const dq8::Weights& w, const int8_t* q, int ldq, co
   p.layout = layout;
 }
 
+// Wide kernel: split the tile grid into gm x gn regions, gm * gn = 8, one per
+// XCD.  An XCD then fetches 1/gm of the activation rows and 1/gn of the weight
+// columns into its L2, so the launch fetches about gn*|A| + gm*|B| bytes from
+// beyond L2; pick the split that minimises it.  0 = no split (tile counts that
+// no split divides).
+int xcd_rows_split(int row_tiles, int col_tiles, size_t a_bytes, size_t b_bytes) {
+  int best = 0;
+  size_t best_cost = 0;
+  for (int gm = 1; gm <= 8; gm *= 2) {
+    const int gn = 8 / gm;
+    if (row_tiles % gm != 0 || col_tiles % gn != 0) continue;
+    const size_t cost = (size_t)gn * a_bytes + (size_t)gm * b_bytes;
+    if (best == 0 || cost < best_cost) {
+      best = gm;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+// Place a filled projection in a launch of the given kernel kind: its first
+// wave/block, column strips, XCD split and the launch's running total.
+void place_proj(dq8::Proj& p, int kind, dq8::Batch& b) {
+  p.wave_begin = b.total_waves;
+  p.xcd_gm = 0;
+  if (kind == 0) {
+    p.waves_n = p.np / dq8::wide_block_cols();
+    const int row_tiles = (p.m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows();
+    p.xcd_gm = xcd_rows_split(row_tiles, p.waves_n, (size_t)p.m * p.g, (size_t)p.n * p.g);
+    b.total_waves += p.waves_n * row_tiles;
+  } else {
+    p.waves_n = p.np / dq8::skinny_cols();
+    b.total_waves += p.waves_n * dq8::skinny_row_waves(p.m);
+  }
+}
+
 // Quantized inputs are usable by the kernels directly when rows are 16-byte
 // aligned and every group is complete; otherwise they are copied, zero-padded
 // to G*64 bytes per row, into the context workspace.
@@ -158,14 +194,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     }
     dq8::Proj& p = b.p[b.count++];
     fill_proj(p, w, q, ldq, it.scales, it.m, it.bias, it.out, dots, it.layout, it.epilogue);
-    p.wave_begin = b.total_waves;
-    if (kind == 0) {
-      p.waves_n = w.np / dq8::wide_block_cols();
-      b.total_waves += p.waves_n * (int)((it.m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows());
-    } else {
-      p.waves_n = w.np / dq8::skinny_cols();
-      b.total_waves += p.waves_n * dq8::skinny_row_waves((int)it.m);
-    }
+    place_proj(p, kind, b);
   }
   for (int kind = 0; kind < 3; ++kind) {
     if (batch[kind].count == 0) continue;
@@ -361,11 +390,9 @@ dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, 
   b.count = 1;
   dq8::Proj& p = b.p[0];
   fill_proj(p, w->w, q, (int)ldq, xs, m, bias, out, nullptr, layout, epilogue);
-  p.wave_begin = 0;
+  b.total_waves = 0;
   const int kind = m > 32 ? 0 : m <= 16 ? 1 : 2;
-  p.waves_n = kind == 0 ? w->w.np / dq8::wide_block_cols() : w->w.np / dq8::skinny_cols();
-  b.total_waves = kind == 0 ? p.waves_n * (int)((m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows())
-                            : p.waves_n * dq8::skinny_row_waves((int)m);
+  place_proj(p, kind, b);
   return from_hip(dq8::launch_linear(b, kind, false, s));
 }
 

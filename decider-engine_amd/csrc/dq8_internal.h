@@ -38,7 +38,8 @@ struct Proj {
   int epilogue;       // 0 write, 1 add, 2 swiglu
   int layout;         // 0 rows [M][N], 1 columns [N][M]
   int wave_begin;     // first wave (skinny) or block (wide) of this projection in the launch
-  int waves_n;        // column strips (skinny: 32 wide, wide: one block tile wide)
+  int waves_n;        // column strips (skinny: skinny_cols() wide, wide: one block tile wide)
+  int xcd_gm;         // wide: row bands of the per-XCD tile regions (1, 2, 4, 8), 0 = row-major order
 };
 
 struct Batch {

@@ -56,16 +56,33 @@ __device__ __forceinline__ float silu(float x) {
   return x * (1.0f / (1.0f + e));
 }
 
-// Epilogue::store (tensor.rs:92-99) through write_columns (tensor.rs:272-288).
-__device__ __forceinline__ void store_out(const Proj& P, int row, int col, float y) {
+// Epilogue::store (tensor.rs:92-99) through write_columns (tensor.rs:272-288)
+// for E values of one lane at (row[e], col[e]); elements outside m x n are
+// skipped.  Layout and epilogue are uniform, so they are branched on once, and
+// every old value an Add/SwiGlu store reads is loaded before the first store.
+template <int E>
+__device__ __forceinline__ void store_tile(const Proj& P, const int (&row)[E], const int (&col)[E],
+                                           const float (&y)[E]) {
   if (P.layout == 1) {
-    P.out[(size_t)col * P.m + row] = y;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (row[e] < P.m && col[e] < P.n) P.out[(size_t)col[e] * P.m + row[e]] = y[e];
     return;
   }
-  float* dst = P.out + (size_t)row * P.n + col;
-  if (P.epilogue == 0) *dst = y;
-  else if (P.epilogue == 1) *dst = *dst + y;
-  else *dst = silu(*dst) * y;
+  if (P.epilogue == 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (row[e] < P.m && col[e] < P.n) P.out[(size_t)row[e] * P.n + col[e]] = y[e];
+    return;
+  }
+  float old[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    old[e] = row[e] < P.m && col[e] < P.n ? P.out[(size_t)row[e] * P.n + col[e]] : 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (row[e] < P.m && col[e] < P.n)
+      P.out[(size_t)row[e] * P.n + col[e]] = P.epilogue == 1 ? old[e] + y[e] : silu(old[e]) * y[e];
 }
 
 __device__ __forceinline__ int find_proj(const Batch& b, int wave) {
@@ -206,11 +223,26 @@ __global__ void k_pad_rows(const int8_t* __restrict__ q, int rows, int k, int8_t
 // compute.  Groups past the end load clamped operands and the all-zero w scale
 // row G, so p = 0, t = dot * 0 = +-0 and s + t = s (s is never -0).
 
-// Consecutive tiles of a projection go to the same XCD (blocks are dealt to
-// the 8 XCDs round robin), so neighbours share A rows in that XCD's L2.
-__device__ __forceinline__ int xcd_tile(int i, int tiles) {
-  if (tiles % 8 != 0) return i;
-  return (i & 7) * (tiles >> 3) + (i >> 3);
+// Tile (row tile mt, column tile nt) of block i of a projection.  Blocks are
+// dealt to the 8 XCDs round robin, so blocks i, i+8, ... share one XCD and its
+// L2.  With P.xcd_gm = gm the tile grid is cut into gm x (8/gm) regions and
+// XCD i%8 walks region i%8, column tiles fastest: it touches 1/gm of the
+// activation rows and 1/(8/gm) of the weight columns.  The map is a bijection
+// on [0, row_tiles * col_tiles) (the host picks gm dividing both counts).
+__device__ __forceinline__ void tile_of(const Proj& P, int i, int row_tiles, int& mt, int& nt) {
+  const int col_tiles = P.waves_n;
+  if (P.xcd_gm == 0) {
+    mt = i / col_tiles;
+    nt = i - mt * col_tiles;
+    return;
+  }
+  const int gm = P.xcd_gm, gn = 8 / gm;
+  const int rm = row_tiles / gm, rn = col_tiles / gn;  // region size in tiles
+  const int x = i & 7, j = i >> 3;
+  const int xa = x / gn, xb = x - xa * gn;
+  const int lm = j / rn;
+  mt = xa * rm + lm;
+  nt = xb * rn + (j - lm * rn);
 }
 
 // Direct global->LDS loads.  They are issued through inline assembly so the
@@ -292,10 +324,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_linear_wide(Batch b) {
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int blk = blockIdx.x;
-  const Proj& P = b.p[find_proj(b, blk)];
-  const int tiles = P.waves_n * ((P.m + BM - 1) / BM);
-  const int t = xcd_tile(blk - P.wave_begin, tiles);
-  const int mt = t / P.waves_n, nt = t - mt * P.waves_n;
+  const Proj P = b.p[find_proj(b, blk)];  // by value: fields stay in registers across the stores
+  int mt, nt;
+  tile_of(P, blk - P.wave_begin, (P.m + BM - 1) / BM, mt, nt);
   const int m0 = mt * BM, n0 = nt * BN;
   const int G = P.g;
 
@@ -430,271 +461,27 @@ __global__ __launch_bounds__(64 * WM * WN) void k_linear_wide(Batch b) {
   wait_vmcnt<0>();
   if constexpr (!DOTS) {
     const int mw = m0 + WR * wm, nw = n0 + WC * wn;
+    // y = s + bias[col], or s + 0.0f without a bias (tensor.rs:437)
+    float bias[CT];
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      const int col = nw + 32 * c + (lane & 31);
+      bias[c] = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
+    }
+    constexpr int E = NP * 32;
+    int rows[E], cols[E];
+    float y[E];
 #pragma unroll
     for (int j = 0; j < NP; ++j)
 #pragma unroll
       for (int v = 0; v < 32; ++v) {
         const int blk2 = v >> 4, vv = v & 15;
         const int r = RT == 2 ? blk2 : 0, c = RT == 2 ? j : blk2;
-        const int row = mw + 32 * r + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);
-        const int col = nw + 32 * c + (lane & 31);
-        if (row < P.m && col < P.n) store_out(P, row, col, s[j][v] + (P.bias ? P.bias[col] : 0.0f));
+        rows[32 * j + v] = mw + 32 * r + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);
+        cols[32 * j + v] = nw + 32 * c + (lane & 31);
+        y[32 * j + v] = s[j][v] + bias[c];
       }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Software-pipelined wide kernel.  Same data path as k_linear_wide with a
-// 32 x 64 wave tile (one row tile, column tiles c0 and c1 paired in the K=1
-// MFMAs), but the i8 MFMAs of group g+1 are issued before the conversion,
-// product and VALU work of group g, so the dependency latency of one group is
-// covered by the independent MFMAs of the next.  Stage buffers: group g's
-// fragments are read one iteration before its scales; the DMA issued in
-// iteration g refills the buffer of group g-1, which no wave reads any more.
-template <int WM, int WN, int STAGES>
-__global__ __launch_bounds__(64 * WM * WN) void k_linear_wide_sp(Batch b) {
-  constexpr int NW = WM * WN, BM = 32 * WM, BN = 64 * WN;
-  constexpr int AF = BM / 16, BF = BN / 16, NF = AF + BF;
-  constexpr int FPW = NF / NW;
-  constexpr int SCW = (BM + BN) / 64;
-  constexpr int LOADS = FPW + 1;
-  static_assert(NF % NW == 0, "fragments must split evenly over the waves");
-  static_assert(BM % 64 == 0 && BN % 64 == 0 && SCW <= NW, "64 scales per staging wave");
-  static_assert(STAGES >= 3 && STAGES <= 4 && LOADS * (STAGES - 3) <= 63, "pipeline depth");
-  struct Stage {
-    uint8_t frag[NF][kFragBytes];
-    float sc[64 * NW];
-  };
-  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2, st3;
-  auto stage = [&](int i) -> Stage& { return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3; };
-
-  const int lane = threadIdx.x & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const Proj& P = b.p[find_proj(b, blockIdx.x)];
-  const int tiles = P.waves_n * ((P.m + BM - 1) / BM);
-  const int t = xcd_tile(blockIdx.x - P.wave_begin, tiles);
-  const int mt = t / P.waves_n, nt = t - mt * P.waves_n;
-  const int m0 = mt * BM, n0 = nt * BN;
-  const int G = P.g;
-
-  const uint8_t* src[FPW];
-  int stride[FPW];
-#pragma unroll
-  for (int i = 0; i < FPW; ++i) {
-    const int f = wid + i * NW;
-    if (f < AF) {
-      const int row = min(m0 + 32 * (f >> 1) + (lane & 31), P.m - 1);
-      src[i] = reinterpret_cast<const uint8_t*>(P.q) + (size_t)row * P.ldq + 32 * (f & 1) + 16 * (lane >> 5);
-      stride[i] = kGroup;
-    } else {
-      const int fb = f - AF;
-      src[i] = P.wt + ((size_t)(n0 / 32 + (fb >> 1)) * G * 2 + (fb & 1)) * kFragBytes + lane * 16;
-      stride[i] = 2 * kFragBytes;
-    }
-  }
-  const int sw = wid < SCW ? wid : 0;
-  const bool xwave = sw < BM / 64;
-  const float* psc = xwave ? P.xs + (size_t)min(m0 + 64 * sw + lane, P.m - 1) * G
-                           : P.wst + n0 + 64 * (sw - BM / 64) + lane;
-  const size_t sstride = xwave ? 1 : (size_t)P.np;
-  const int slast = xwave ? G - 1 : G;
-  auto issue = [&](Stage& S, int g) {
-    const int gc = min(g, G - 1);
-#pragma unroll
-    for (int i = 0; i < FPW; ++i) dma16(src[i] + (size_t)gc * stride[i], &S.frag[wid + i * NW][0]);
-    dma4(psc + (size_t)min(g, slast) * sstride, &S.sc[64 * wid]);
-  };
-
-  const int wm = wid / WN, wn = wid - (wid / WN) * WN;
-  const int fa = 2 * wm, fbw = AF + 4 * wn;
-
-  v16i magic;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) magic[i] = kMagicBits;
-  v32f zero32;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) zero32[i] = 0.0f;
-  v32f s = zero32;
-
-  auto dots = [&](Stage& S, v16i& d0, v16i& d1) {
-    const v4i* fr = reinterpret_cast<const v4i*>(&S.frag[0][0]);
-    const v4i a0 = fr[(fa + 0) * 64 + lane], a1 = fr[(fa + 1) * 64 + lane];
-    const v4i b0 = fr[(fbw + 0) * 64 + lane], b1 = fr[(fbw + 1) * 64 + lane];
-    const v4i b2 = fr[(fbw + 2) * 64 + lane], b3 = fr[(fbw + 3) * 64 + lane];
-    d0 = mfma_i8(a0, b0, magic);
-    d1 = mfma_i8(a0, b2, magic);
-    d0 = mfma_i8(a1, b1, d0);
-    d1 = mfma_i8(a1, b3, d1);
-  };
-  auto finish = [&](Stage& S, const v16i& d0, const v16i& d1) {
-    const float x = S.sc[32 * wm + (lane & 31)];
-    const float w = S.sc[BM + 64 * wn + lane];
-    const v32f dv = mfma_k1(-kMagic, 1.0f, concat(d0, d1));
-    const v32f pv = mfma_k1(x, w, zero32);
-    s = s + dv * pv;
-  };
-
-  // Prologue: stages 0 .. STAGES-2 in flight; dots of group 0.
-#pragma unroll
-  for (int i = 0; i < STAGES - 1; ++i) {
-    issue(stage(i), i);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  wait_vmcnt<LOADS * (STAGES - 2)>();
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-  v16i c0, c1;
-  dots(stage(0), c0, c1);
-  for (int g0 = 0; g0 < G; g0 += STAGES) {
-#pragma unroll
-    for (int d = 0; d < STAGES; ++d) {
-      const int g = g0 + d;
-      if (g >= G) break;  // uniform over the block
-      // Group g+1 has landed everywhere; every wave is done with group g-1.
-      wait_vmcnt<LOADS * (STAGES - 3)>();
-      __builtin_amdgcn_s_barrier();
-      __builtin_amdgcn_sched_barrier(0);
-      issue(stage((d + STAGES - 1) % STAGES), g + STAGES - 1);
-      __builtin_amdgcn_sched_barrier(0);
-      v16i n0_, n1_;
-      dots(stage((d + 1) % STAGES), n0_, n1_);  // group g+1 (clamped data past the end is unused)
-      finish(stage(d), c0, c1);
-      c0 = n0_;
-      c1 = n1_;
-    }
-  }
-  wait_vmcnt<0>();
-  const int mw = m0 + 32 * wm, nw = n0 + 64 * wn;
-#pragma unroll
-  for (int v = 0; v < 32; ++v) {
-    const int blk2 = v >> 4, vv = v & 15;
-    const int row = mw + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);
-    const int col = nw + 32 * blk2 + (lane & 31);
-    if (row < P.m && col < P.n) store_out(P, row, col, s[v] + (P.bias ? P.bias[col] : 0.0f));
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Skinny projection kernel (M <= 32): weight-streaming.  Each wave owns all
-// (padded) 32 rows x one 32-column tile and walks the groups two at a time
-// (a "step"); the K=1 MFMAs pair group g (block 0) with group g+1 (block 1),
-// and the fp32 sum adds group g's terms before group g+1's.  DEPTH steps of
-// operands are in flight (weights stream from HBM; activations are L2-hot).
-// Groups past the end read clamped operands and the zero w scale row G.
-// This kernel is bandwidth-bound, so the dots start from C = 0 and convert on
-// the VALU (exact: |dot| <= 2^20), which frees the 16 registers of the bias
-// constant for the prefetch ring.
-struct SkinnyFrag {
-  v4i a[4];  // (g,h0) (g,h1) (g+1,h0) (g+1,h1)
-  v4i b[4];
-  float x, w;
-};
-
-template <int DEPTH, bool DOTS>
-__global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
-  const int lane = threadIdx.x & 63;
-  // Wave-uniform (scalar) so the projection record, G and the loop are uniform.
-  const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (wave >= b.total_waves) return;
-  const Proj& P = b.p[find_proj(b, wave)];
-  const int nt = wave - P.wave_begin;
-  const int n0 = nt * 32;
-  const int G = P.g;
-  const int half = lane >> 5;
-  const int steps = (G + 1) >> 1;
-
-  const int row = min(lane & 31, P.m - 1);
-  const int8_t* pa = P.q + (size_t)row * P.ldq + 16 * half;
-  const uint8_t* pb = P.wt + (size_t)nt * G * 2 * kFragBytes + lane * 16;
-  const float* pxs = P.xs + (size_t)row * G;
-  const float* pws = P.wst + n0 + (lane & 31);
-
-  auto load = [&](SkinnyFrag& f, int step) {
-    const int g = 2 * step;
-    const int ga = min(g, G - 1), gb = min(g + 1, G - 1);
-    f.a[0] = load16(pa + ga * kGroup);
-    f.a[1] = load16(pa + ga * kGroup + 32);
-    f.a[2] = load16(pa + gb * kGroup);
-    f.a[3] = load16(pa + gb * kGroup + 32);
-    f.b[0] = load16(pb + (size_t)ga * 2 * kFragBytes);
-    f.b[1] = load16(pb + (size_t)(ga * 2 + 1) * kFragBytes);
-    f.b[2] = load16(pb + (size_t)gb * 2 * kFragBytes);
-    f.b[3] = load16(pb + (size_t)(gb * 2 + 1) * kFragBytes);
-    if constexpr (!DOTS) {
-      const int gl = g + half;  // group carried by this lane's half of the K=1 operands
-      f.x = pxs[min(gl, G - 1)];
-      f.w = pws[(size_t)min(gl, G) * P.np];  // row G of the w scales is zero
-    }
-  };
-
-  const v16i zero16 = {};
-  v32f zero32;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) zero32[i] = 0.0f;
-  v16f s;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s[i] = 0.0f;
-
-  SkinnyFrag ring[DEPTH];
-#pragma unroll
-  for (int d = 0; d < DEPTH; ++d) {
-    // Issue the prologue in ring order so the loop's wait counts hold on entry too.
-    load(ring[d], d);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  for (int s0 = 0; s0 < steps; s0 += DEPTH) {
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int step = s0 + d;
-      const SkinnyFrag& c = ring[d];
-      v16i d0 = mfma_i8(c.a[0], c.b[0], zero16);
-      v16i d1 = mfma_i8(c.a[2], c.b[2], zero16);
-      d0 = mfma_i8(c.a[1], c.b[1], d0);
-      d1 = mfma_i8(c.a[3], c.b[3], d1);
-      v32f pv;
-      if constexpr (!DOTS) pv = mfma_k1(c.x, c.w, zero32);
-      // Refill the slot once every operand of it is consumed: the loads reuse
-      // the slot's registers (no loop-carried copies) and have DEPTH - 1 steps to land.
-      __builtin_amdgcn_sched_barrier(0);
-      load(ring[d], step + DEPTH);
-      __builtin_amdgcn_sched_barrier(0);
-      if constexpr (DOTS) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int g = 2 * step + t;
-          if (g >= G) break;
-          const v16i& dd = t == 0 ? d0 : d1;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int r = 8 * (v >> 2) + 4 * half + (v & 3);
-            const int col = n0 + (lane & 31);
-            if (r < P.m && col < P.n) P.dots[((size_t)r * P.n + col) * G + g] = dd[v];
-          }
-        }
-      } else {
-        v32f dv;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          dv[v] = (float)d0[v];
-          dv[16 + v] = (float)d1[v];
-        }
-        const v32f t = dv * pv;
-        s = s + __builtin_shufflevector(t, t, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
-        s = s + __builtin_shufflevector(t, t, 16, 17, 18, 19, 20, 21, 22, 23, 24, 25, 26, 27, 28, 29, 30, 31);
-      }
-    }
-  }
-  if constexpr (!DOTS) {
-    const int col = n0 + (lane & 31);
-    if (col < P.n) {
-      const float bias = P.bias ? P.bias[col] : 0.0f;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = 8 * (v >> 2) + 4 * half + (v & 3);
-        if (r < P.m) store_out(P, r, col, s[v] + bias);
-      }
-    }
+    store_tile(P, rows, cols, y);
   }
 }
 
@@ -726,7 +513,7 @@ __global__ __launch_bounds__(256) void k_linear_skinny16(Batch b) {
   const int lane = threadIdx.x & 63;
   const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wave >= b.total_waves) return;
-  const Proj& P = b.p[find_proj(b, wave)];
+  const Proj P = b.p[find_proj(b, wave)];
   const int rtiles = (P.m + 15) >> 4;
   const int w_local = wave - P.wave_begin;
   const int nt = w_local / rtiles;  // 16-column strip
@@ -792,14 +579,16 @@ __global__ __launch_bounds__(256) void k_linear_skinny16(Batch b) {
   }
   if constexpr (!DOTS) {
     const int col = c0 + (lane & 15);
-    if (col < P.n) {
-      const float bias = P.bias ? P.bias[col] : 0.0f;
+    const float bias = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
+    int rows[4], cols[4];
+    float y[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = r0 + 4 * (lane >> 4) + v;
-        if (row < P.m) store_out(P, row, col, s[v] + bias);
-      }
+    for (int v = 0; v < 4; ++v) {
+      rows[v] = r0 + 4 * (lane >> 4) + v;
+      cols[v] = col;
+      y[v] = s[v] + bias;
     }
+    store_tile(P, rows, cols, y);
   }
 }
 
@@ -837,32 +626,19 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
   return hipGetLastError();
 }
 
-#ifndef DQ8_WIDE_SP
-#define DQ8_WIDE_SP 0
-#endif
-#ifndef DQ8_SKINNY_DEPTH
-#define DQ8_SKINNY_DEPTH 4
-#endif
-#ifndef DQ8_SKINNY16
-#define DQ8_SKINNY16 1
-#endif
 #ifndef DQ8_SKINNY16_DEPTH
 #define DQ8_SKINNY16_DEPTH 4
 #endif
-int skinny_cols() { return DQ8_SKINNY16 ? 16 : 32; }
-int skinny_row_waves(int m) { return DQ8_SKINNY16 ? (m + 15) / 16 : 1; }
-int wide_block_rows() { return DQ8_WIDE_SP ? 32 * DQ8_WIDE_WM : 32 * DQ8_WIDE_RT * DQ8_WIDE_WM; }
-int wide_block_cols() { return DQ8_WIDE_SP ? 64 * DQ8_WIDE_WN : 32 * DQ8_WIDE_CT * DQ8_WIDE_WN; }
+int skinny_cols() { return 16; }
+int skinny_row_waves(int m) { return (m + 15) / 16; }
+int wide_block_rows() { return 32 * DQ8_WIDE_RT * DQ8_WIDE_WM; }
+int wide_block_cols() { return 32 * DQ8_WIDE_CT * DQ8_WIDE_WN; }
 
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
   if (b.total_waves == 0) return hipSuccess;
   if (kind == 0) {
     // total_waves counts blocks for the wide kernel
     constexpr int threads = 64 * DQ8_WIDE_WM * DQ8_WIDE_WN;
-    if (DQ8_WIDE_SP && !dots) {
-      k_linear_wide_sp<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_STAGES><<<b.total_waves, threads, 0, s>>>(b);
-      return hipGetLastError();
-    }
     if (dots)
       k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_CVT_VALU, true>
           <<<b.total_waves, threads, 0, s>>>(b);
@@ -872,15 +648,8 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
     return hipGetLastError();
   }
   const unsigned blocks = blocks_for(b.total_waves, 4);
-  if (DQ8_SKINNY16) {
-    if (dots) k_linear_skinny16<DQ8_SKINNY16_DEPTH, true><<<blocks, 256, 0, s>>>(b);
-    else k_linear_skinny16<DQ8_SKINNY16_DEPTH, false><<<blocks, 256, 0, s>>>(b);
-    return hipGetLastError();
-  }
-  {
-    if (dots) k_linear_skinny<DQ8_SKINNY_DEPTH, true><<<blocks, 256, 0, s>>>(b);
-    else k_linear_skinny<DQ8_SKINNY_DEPTH, false><<<blocks, 256, 0, s>>>(b);
-  }
+  if (dots) k_linear_skinny16<DQ8_SKINNY16_DEPTH, true><<<blocks, 256, 0, s>>>(b);
+  else k_linear_skinny16<DQ8_SKINNY16_DEPTH, false><<<blocks, 256, 0, s>>>(b);
   return hipGetLastError();
 }
 
