@@ -88,10 +88,11 @@ dq8_status make_weights(dq8_ctx* ctx, size_t n, size_t k, dq8_weights** out) {
 }
 
 // Fill a launch item.  q must already satisfy the kernel's requirements.
-void fill_proj(dq8::Proj& p, const dq8::Weights& w, const int8_t* q, int ldq, const float* xs, size_t m,
+void fill_proj(dq8::Proj& p, const dq8::Weights& w, const int8_t* q, int ldq, const float* xs, int ldxs, size_t m,
                const float* bias, float* out, int32_t* dots, int layout, int epilogue) {
   p.q = q;
   p.xs = xs;
+  p.ldxs = ldxs;
   p.wt = w.values;
   p.wst = w.scales;
   p.bias = bias;
@@ -147,6 +148,14 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b) {
 // to G*64 bytes per row, into the context workspace.
 bool needs_pad(const dq8::Weights& w, const int8_t* q) { return w.k % kGroup != 0 || !aligned(q, 16); }
 size_t pad_bytes(const dq8::Weights& w, size_t m) { return (m * (size_t)w.g * kGroup + 255) / 256 * 256; }
+// The wide kernel loads x scales in 16-byte pieces of 4 groups: rows must be
+// 16-byte aligned with a stride that is a multiple of 4 floats.  Otherwise they
+// are copied into the workspace with the stride rounded up.
+int padded_groups(const dq8::Weights& w) { return (w.g + 3) / 4 * 4; }
+bool needs_xs_pad(const dq8::Weights& w, const float* xs) { return w.g % 4 != 0 || !aligned(xs, 16); }
+size_t xs_pad_bytes(const dq8::Weights& w, size_t m) {
+  return (m * (size_t)padded_groups(w) * sizeof(float) + 255) / 256 * 256;
+}
 
 dq8_status check_item_args(const dq8_weights* w, const int8_t* q, const float* scales, size_t m, float* out,
                            dq8_layout layout, dq8_epilogue epilogue) {
@@ -161,8 +170,12 @@ dq8_status check_item_args(const dq8_weights* w, const int8_t* q, const float* s
 // Split items by kernel kind and launch.  Items with m == 0 do nothing (tensor.rs:152-154).
 dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, int32_t* dots, hipStream_t s) {
   size_t need = 0;
-  for (size_t i = 0; i < count; ++i)
-    if (items[i].m && needs_pad(items[i].w->w, items[i].q)) need += pad_bytes(items[i].w->w, items[i].m);
+  for (size_t i = 0; i < count; ++i) {
+    if (!items[i].m) continue;
+    if (needs_pad(items[i].w->w, items[i].q)) need += pad_bytes(items[i].w->w, items[i].m);
+    if (!dots && items[i].m > 32 && needs_xs_pad(items[i].w->w, items[i].scales))
+      need += xs_pad_bytes(items[i].w->w, items[i].m);
+  }
   if (need) {
     dq8_status st = ensure_work(ctx, need);
     if (st != DQ8_OK) return st;
@@ -192,8 +205,18 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
       q = dst;
       offset += pad_bytes(w, it.m);
     }
+    const float* xs = it.scales;
+    int ldxs = w.g;
+    if (!dots && kind == 0 && needs_xs_pad(w, it.scales)) {  // the dots kernels read no scales
+      float* dst = (float*)((char*)ctx->work + offset);
+      ldxs = padded_groups(w);
+      hipError_t e = dq8::launch_pad_scales(it.scales, (int)it.m, w.g, dst, ldxs, s);
+      if (e != hipSuccess) return from_hip(e);
+      xs = dst;
+      offset += xs_pad_bytes(w, it.m);
+    }
     dq8::Proj& p = b.p[b.count++];
-    fill_proj(p, w, q, ldq, it.scales, it.m, it.bias, it.out, dots, it.layout, it.epilogue);
+    fill_proj(p, w, q, ldq, xs, ldxs, it.m, it.bias, it.out, dots, it.layout, it.epilogue);
     place_proj(p, kind, b);
   }
   for (int kind = 0; kind < 3; ++kind) {
@@ -280,7 +303,8 @@ dq8_status dq8_weights_from_f32(dq8_ctx* ctx, const float* w, size_t n, size_t k
   hipError_t e = hipMalloc(&values, n * k);
   if (e == hipSuccess) e = hipMalloc(&scales, n * g * sizeof(float));
   // Data::quantize has the same per-group formula as QuantizedInputs::new (weights.rs:117-136).
-  if (e == hipSuccess) e = dq8::launch_quantize(w, (int)n, (int)k, (int8_t*)values, (int)k, scales, nullptr, s);
+  if (e == hipSuccess)
+    e = dq8::launch_quantize(w, (int)n, (int)k, (int8_t*)values, (int)k, scales, (int)groups_of(k), nullptr, s);
   dq8_status st = from_hip(e);
   if (st == DQ8_OK) st = dq8_weights_from_quantized(ctx, values, scales, n, k, stream, out);
   (void)hipStreamSynchronize(s);
@@ -324,7 +348,7 @@ dq8_status dq8_quantize(dq8_ctx* ctx, const float* x, size_t m, size_t k, int8_t
   uint32_t* flag = nonfinite ? nonfinite : ctx->flag;
   hipError_t e = hipSuccess;
   if (!nonfinite) e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
-  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, (int)k, q, (int)k, scales, flag, s);
+  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, (int)k, q, (int)k, scales, (int)groups_of(k), flag, s);
   if (e != hipSuccess) return from_hip(e);
   if (nonfinite) return DQ8_OK;
   uint32_t host = 0;
@@ -375,12 +399,13 @@ dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, 
   hipStream_t s = (hipStream_t)stream;
   const size_t ldq = (size_t)w->w.g * kGroup;
   const size_t qbytes = (m * ldq + 255) / 256 * 256;
-  dq8_status st = ensure_work(ctx, qbytes + m * w->w.g * sizeof(float));
+  const int ldxs = padded_groups(w->w);
+  dq8_status st = ensure_work(ctx, qbytes + xs_pad_bytes(w->w, m));
   if (st != DQ8_OK) return st;
   int8_t* q = (int8_t*)ctx->work;
   float* xs = (float*)((char*)ctx->work + qbytes);
   hipError_t e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
-  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, w->w.k, q, (int)ldq, xs, ctx->flag, s);
+  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, w->w.k, q, (int)ldq, xs, ldxs, ctx->flag, s);
   uint32_t host = 0;
   if (e == hipSuccess) e = hipMemcpyAsync(&host, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -389,7 +414,7 @@ dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, 
   dq8::Batch b;
   b.count = 1;
   dq8::Proj& p = b.p[0];
-  fill_proj(p, w->w, q, (int)ldq, xs, m, bias, out, nullptr, layout, epilogue);
+  fill_proj(p, w->w, q, (int)ldq, xs, ldxs, m, bias, out, nullptr, layout, epilogue);
   b.total_waves = 0;
   const int kind = m > 32 ? 0 : m <= 16 ? 1 : 2;
   place_proj(p, kind, b);

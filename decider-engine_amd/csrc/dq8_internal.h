@@ -28,13 +28,13 @@ struct Weights {
 // every byte up to G*64 of each row readable (zero past K).
 struct Proj {
   const int8_t* q;
-  const float* xs;    // [M][G]
+  const float* xs;    // [M][ldxs], ldxs >= G
   const uint8_t* wt;  // Weights::values
   const float* wst;   // Weights::scales
   const float* bias;  // [N] or null
   float* out;
   int32_t* dots;      // debug output [M][N][G] (dots kernels only)
-  int m, ldq, g, n, np;
+  int m, ldq, ldxs, g, n, np;
   int epilogue;       // 0 write, 1 add, 2 swiglu
   int layout;         // 0 rows [M][N], 1 columns [N][M]
   int wave_begin;     // first wave (skinny) or block (wide) of this projection in the launch
@@ -49,11 +49,13 @@ struct Batch {
 };
 
 // Kernel launchers (dq8_kernels.hip).  All return hipError_t of the launch.
-hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, float* scales,
+// scales row stride lds >= G = ceil(k / 64)
+hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
                            uint32_t* nonfinite, hipStream_t s);
 hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int k, Weights* w, hipStream_t s);
 hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipStream_t s);
 hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ldq, hipStream_t s);
+hipError_t launch_pad_scales(const float* xs, int rows, int g, float* dst, int ld, hipStream_t s);
 // Kind: 0 wide (M > 32), 1 skinny with M <= 16, 2 skinny with 16 < M <= 32.
 // dots selects the debug kernel.
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s);

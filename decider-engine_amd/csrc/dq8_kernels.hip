@@ -99,7 +99,7 @@ __device__ __forceinline__ int find_proj(const Batch& b, int wave) {
 // max-reduction over its 16 lanes.  The division is the IEEE one and roundf
 // rounds half away from zero, as f32::round.
 __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, int rows, int k, int8_t* __restrict__ q,
-                                                  int ldq, float* __restrict__ scales, uint32_t* nonfinite) {
+                                                  int ldq, float* __restrict__ scales, int lds, uint32_t* nonfinite) {
   const int lane = threadIdx.x & 63;
   const int chunks = (k + 255) >> 8;
   const long item = (long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, i
   }
   const int group = (chunk * 256 + (lane & ~15) * 4) / kGroup;
   const int groups = (k + kGroup - 1) / kGroup;
-  if ((lane & 15) == 0 && group < groups) scales[(size_t)row * groups + group] = scale;
+  if ((lane & 15) == 0 && group < groups) scales[(size_t)row * lds + group] = scale;
 }
 
 // Reference layout -> fragment layout (see Weights in dq8_internal.h).
@@ -198,6 +198,14 @@ __global__ void k_export_scales(const float* __restrict__ wst, int n, int g, int
 }
 
 // Copy q [rows][k] into dst [rows][ldq] with zero padding (ldq = G*64).
+// xs [rows][g] -> dst [rows][ld] (ld >= g), zero past g.
+__global__ void k_pad_scales(const float* __restrict__ xs, int rows, int g, float* __restrict__ dst, int ld) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)rows * ld) return;
+  const int row = (int)(i / ld), c = (int)(i - (long)row * ld);
+  dst[i] = c < g ? xs[(size_t)row * g + c] : 0.0f;
+}
+
 __global__ void k_pad_rows(const int8_t* __restrict__ q, int rows, int k, int8_t* __restrict__ dst, int ldq) {
   long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (long)rows * ldq) return;
@@ -206,22 +214,7 @@ __global__ void k_pad_rows(const int8_t* __restrict__ q, int rows, int k, int8_t
 }
 
 // ---------------------------------------------------------------------------
-// Wide projection kernel (M > 32), LDS-staged.  A block of WM x WN waves owns
-// a (64*WM) x (64*WN) output tile; each wave owns 64 x 64 of it: row tiles
-// r0, r1 (32 rows each) x column tiles j0, j1.  Per group, for each column
-// tile j the pair (r0, j), (r1, j) shares one conversion MFMA and one product
-// MFMA: A lane l carries the x scale of row m0 + l, B lane l the w scale of
-// column n0 + 32j + l%32.
-//
-// Operands reach LDS by direct global->LDS loads (global_load_lds_dwordx4:
-// lane l's 16 bytes land at base + 16*l, i.e. fragments stay in lane order and
-// LDS reads are conflict-free ds_read_b128).  STAGES groups are in flight in
-// an LDS ring.  Iteration g: wait for this wave's loads of group g
-// (vmcnt <= loads of the STAGES-2 newer groups), barrier (every wave's loads
-// of group g have landed and every wave is done reading group g-1), issue the
-// loads of group g+STAGES-1 into group g-1's buffer, then read group g and
-// compute.  Groups past the end load clamped operands and the all-zero w scale
-// row G, so p = 0, t = dot * 0 = +-0 and s + t = s (s is never -0).
+// Wide projection kernel (M > 32): helpers.
 
 // Tile (row tile mt, column tile nt) of block i of a projection.  Blocks are
 // dealt to the 8 XCDs round robin, so blocks i, i+8, ... share one XCD and its
@@ -253,16 +246,18 @@ __device__ __forceinline__ void tile_of(const Proj& P, int i, int row_tiles, int
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }
-__device__ __forceinline__ void dma16(const void* src, const void* lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+// The address is split into a wave-uniform 64-bit base (SGPRs, advanced per
+// group on the scalar unit) and a fixed 32-bit per-lane offset.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, const void* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
-               : "s"(lds_offset(lds)), "v"(src)
+               : "s"(lds_offset(lds)), "v"(off), "s"(base)
                : "memory");
 }
-__device__ __forceinline__ void dma4(const void* src, const void* lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+__device__ __forceinline__ void dma4s(const void* base, uint32_t off, const void* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                :
-               : "s"(lds_offset(lds)), "v"(src)
+               : "s"(lds_offset(lds)), "v"(off), "s"(base)
                : "memory");
 }
 template <int N>
@@ -271,10 +266,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Launch shape of the wide kernel (tunable at build time):
-//   WM x WN waves per block, each wave (32*RT) rows x (32*CT) columns;
-//   STAGES groups in flight in LDS; CVT_VALU converts the dots on the VALU
-//   (C = 0) instead of the K=1 MFMA (C = bias bits).
+// Launch shape of the wide kernel (tunable at build time): WM x WN waves per
+// block, each wave (32*RT) rows x (32*CT) columns; STAGES groups in flight in
+// LDS; x-scale chunk of XCH groups; A-slab swizzle SWZ (0: for 16-lane LDS
+// phases, 1: for 8-lane); WPE > 0 caps registers for that many waves per SIMD.
 #ifndef DQ8_WIDE_WM
 #define DQ8_WIDE_WM 2
 #endif
@@ -288,89 +283,172 @@ __device__ __forceinline__ void wait_vmcnt() {
 #define DQ8_WIDE_CT 2
 #endif
 #ifndef DQ8_WIDE_STAGES
-#define DQ8_WIDE_STAGES 4
+#define DQ8_WIDE_STAGES 2
 #endif
-#ifndef DQ8_WIDE_CVT_VALU
-#define DQ8_WIDE_CVT_VALU 0
+#ifndef DQ8_WIDE_XCH
+#define DQ8_WIDE_XCH 16
+#endif
+#ifndef DQ8_WIDE_SWZ
+#define DQ8_WIDE_SWZ 1
+#endif
+#ifndef DQ8_WIDE_WPE
+#define DQ8_WIDE_WPE 0
 #endif
 
-// A wave's 32x32 tiles are processed in pairs that share one conversion and one
-// product MFMA (blocks 0 and 1 of v_mfma_f32_32x32x1_2b_f32):
+// ---------------------------------------------------------------------------
+// Wide projection kernel (M > 32), LDS-staged.  A block of WM x WN waves owns
+// a (32*RT*WM) x (32*CT*WN) output tile; each wave owns (32*RT) x (32*CT) of
+// it.  Per group, a wave's 32x32 tiles are processed in pairs that share one
+// conversion MFMA and one product MFMA (blocks 0 and 1 of
+// v_mfma_f32_32x32x1_2b_f32):
 //   RT == 2: pair j = row tiles (0, 1) at column tile j;  A lane l: x of row l,
 //            B lane l: w of column 32j + l%32.
 //   RT == 1: one pair = column tiles (0, 1) at the single row tile;  A lane l:
 //            x of row l%32, B lane l: w of column l.
-template <int WM, int WN, int RT, int CT, int STAGES, bool CVT_VALU, bool DOTS>
-__global__ __launch_bounds__(64 * WM * WN) void k_linear_wide(Batch b) {
-  constexpr int NW = WM * WN, WR = 32 * RT, WC = 32 * CT;  // wave tile WR x WC
+//
+// Operands reach LDS by direct global->LDS loads (global_load_lds_*: lane l's
+// bytes land at base + size*l).  The cost of such a load is set by the number
+// of distinct cache lines its 64 lanes touch, not by its bytes, so:
+//  * A: per group, 16-row x 64-byte slabs (16 lines per 1 KB load).  Lane l of
+//    the load fetches row l/4, 16-byte chunk (l%4) ^ f(row) and lands at slot
+//    l, so the MFMA operand reads (row R, chunk c) from slot
+//    4*(R%16) + (c ^ f(R%16)) of slab R/16: the XOR keeps ds_read_b128 free of
+//    bank conflicts (f = (r>>2)&3 for 16-lane phases, (r>>1)&3 for 8-lane).
+//  * x scales: once per XCH groups, as row slabs of XCH*4 bytes (one load
+//    covers 256/XCH rows), double-buffered; pieces of 4 groups are XOR-swizzled
+//    by row like the A chunks.  Pieces past G load an in-bounds dummy (G % 4
+//    == 0 and ldxs % 4 == 0 are required; the host pads xs otherwise).
+//  * B: 1 KB weight fragments (8 lines each) and w scales (contiguous).
+// Every wave issues the same number of loads per group (the last slot is
+// padded with a duplicate w-scale load), so the vmcnt waits are compile-time
+// constants; an x-scale chunk is issued just before the group loads of its
+// first group and is therefore complete when that group is.
+//
+// STAGES groups are in flight in an LDS ring.  Iteration g: wait for this
+// wave's loads of group g (vmcnt <= loads of the STAGES-2 newer groups),
+// barrier (every wave's loads of group g have landed and every wave is done
+// reading group g-1), issue the loads of group g+STAGES-1 into group g-1's
+// buffer, then read group g and compute.  Groups past the end load clamped
+// operands and the all-zero w-scale row G; they are never computed on.
+#if DQ8_WIDE_WPE > 0
+#define DQ8_WIDE_ATTR __attribute__((amdgpu_waves_per_eu(DQ8_WIDE_WPE, DQ8_WIDE_WPE)))
+#else
+#define DQ8_WIDE_ATTR
+#endif
+template <int WM, int WN, int RT, int CT, int STAGES, int XCH, int SWZ, bool DOTS>
+__global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batch b) {
+  constexpr int NW = WM * WN, WR = 32 * RT, WC = 32 * CT;
   constexpr int BM = WR * WM, BN = WC * WN;
-  constexpr int AF = BM / 16, BF = BN / 16, NF = AF + BF;  // 1 KB fragments per group
-  constexpr int FPW = NF / NW;
-  constexpr int SCW = (BM + BN) / 64;           // waves holding real scales
-  constexpr int LOADS = FPW + (DOTS ? 0 : 1);   // DMA instructions per wave per group
-  constexpr int NP = RT == 2 ? CT : 1;          // pairs per wave
-  static_assert(NF % NW == 0, "fragments must split evenly over the waves");
-  static_assert(BM % 64 == 0 && BN % 64 == 0 && SCW <= NW, "64 scales per staging wave");
+  constexpr int AS = BM / 16;                  // A slabs per group
+  constexpr int BF = BN / 16;                  // B fragments per group
+  constexpr int WSD = DOTS ? 0 : BN / 64;      // w-scale loads per group
+  constexpr int L16 = (AS + BF) / NW;          // 16-byte loads per wave per group
+  constexpr int LOADS = L16 + (DOTS ? 0 : 1);  // + one w-scale load (or duplicate)
+  constexpr int PPR = XCH / 4;                 // 16-byte x-scale pieces per row
+  constexpr int RPD = 64 / PPR;                // rows per x-scale load
+  constexpr int XD = BM / RPD;                 // x-scale loads per chunk
+  constexpr int XPW = XD / NW;                 // ... per wave
+  constexpr int NP = RT == 2 ? CT : 1;         // tile pairs per wave
+  static_assert((AS + BF) % NW == 0, "16-byte loads must split evenly over the waves");
+  static_assert(WSD <= NW && XD % NW == 0 && XPW >= 1, "scale loads per wave");
+  static_assert(XCH == 16 || XCH == 32, "x-scale chunk");
   static_assert((RT == 2 && (CT == 1 || CT == 2)) || (RT == 1 && CT == 2), "supported wave tiles");
-  static_assert(STAGES >= 2 && STAGES <= 4 && LOADS * (STAGES - 2) <= 63, "pipeline depth");
-  // One LDS object per stage, always indexed by compile-time constants.
+  static_assert(STAGES >= 2 && STAGES <= 4 && LOADS * (STAGES - 2) + XPW <= 63, "pipeline depth");
   struct Stage {
-    uint8_t frag[NF][kFragBytes];
-    float sc[64 * NW];  // x scales of the BM rows, w scales of the BN columns, then padding
+    uint8_t frag[AS + BF][kFragBytes];  // A slabs, then B fragments
+    float ws[BN];
+  };
+  struct XChunk {
+    uint8_t d[XD][kFragBytes];
   };
   __shared__ __attribute__((aligned(16))) Stage st0, st1, st2, st3;
+  __shared__ __attribute__((aligned(16))) XChunk xc[DOTS ? 1 : 2];
   auto stage = [&](int i) -> Stage& { return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3; };
 
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int blk = blockIdx.x;
-  const Proj P = b.p[find_proj(b, blk)];  // by value: fields stay in registers across the stores
+  const Proj P = b.p[find_proj(b, blk)];
   int mt, nt;
   tile_of(P, blk - P.wave_begin, (P.m + BM - 1) / BM, mt, nt);
   const int m0 = mt * BM, n0 = nt * BN;
   const int G = P.g;
+  auto swz = [](int r) { return SWZ == 0 ? (r >> 2) & 3 : (r >> 1) & 3; };
 
-  // Global sources of this wave's fragments: A (row tile, half) or B (column tile, half).
-  const uint8_t* src[FPW];
-  int stride[FPW];
+  // 16-byte loads: slot k of this wave is load i = k*NW + wid (A slab i, or B
+  // fragment i - AS), landing at frag[i].  Address = uniform base + group *
+  // stride (scalar) + a fixed lane offset.
+  const uint8_t* sbase[L16];
+  uint32_t loff[L16];
+  int stride[L16];
 #pragma unroll
-  for (int i = 0; i < FPW; ++i) {
-    const int f = wid + i * NW;
-    if (f < AF) {
-      const int row = min(m0 + 32 * (f >> 1) + (lane & 31), P.m - 1);
-      src[i] = reinterpret_cast<const uint8_t*>(P.q) + (size_t)row * P.ldq + 32 * (f & 1) + 16 * (lane >> 5);
-      stride[i] = kGroup;
+  for (int k = 0; k < L16; ++k) {
+    const int i = k * NW + wid;
+    if (i < AS) {
+      const int rr = lane >> 2;
+      const int r0 = min(m0 + 16 * i, P.m - 1);
+      const int row = min(m0 + 16 * i + rr, P.m - 1);
+      sbase[k] = reinterpret_cast<const uint8_t*>(P.q) + (size_t)r0 * P.ldq;
+      loff[k] = (uint32_t)((row - r0) * P.ldq + 16 * ((lane & 3) ^ swz(rr)));
+      stride[k] = kGroup;
     } else {
-      const int fb = f - AF;
-      src[i] = P.wt + ((size_t)(n0 / 32 + (fb >> 1)) * G * 2 + (fb & 1)) * kFragBytes + lane * 16;
-      stride[i] = 2 * kFragBytes;
+      const int fb = i - AS;
+      sbase[k] = P.wt + ((size_t)(n0 / 32 + (fb >> 1)) * G * 2 + (fb & 1)) * kFragBytes;
+      loff[k] = (uint32_t)lane * 16;
+      stride[k] = 2 * kFragBytes;
     }
   }
-  // Scales: the first BM/64 waves stage x scales of 64 rows each, the next BN/64
-  // waves w scales of 64 columns; the rest load a harmless duplicate into the
-  // padding so that every wave issues the same number of loads.  x scales clamp
-  // to the last group, w scales run into the zero row G.
-  const int sw = wid < SCW ? wid : 0;
-  const bool xwave = sw < BM / 64;
-  const float* psc = xwave ? P.xs + (size_t)min(m0 + 64 * sw + lane, P.m - 1) * G
-                           : P.wst + n0 + 64 * (sw - BM / 64) + lane;
-  const size_t sstride = xwave ? 1 : (size_t)P.np;
-  const int slast = xwave ? G - 1 : G;
+  // w scales: wave w < WSD loads columns 64w .. 64w+63; the others repeat wave
+  // w % WSD's load (same data, same place).  Row G of the scales is zero.
+  const int ww = WSD > 0 ? wid % (WSD > 0 ? WSD : 1) : 0;
+  const float* wsbase = P.wst + n0 + 64 * ww;
+  // x-scale pieces: load d = k*NW + wid of a chunk covers rows RPD*d .. RPD*d+RPD-1;
+  // lane l fetches row l/PPR, piece (l%PPR) ^ (row%PPR).
 
   auto issue = [&](Stage& S, int g) {
     const int gc = min(g, G - 1);
 #pragma unroll
-    for (int i = 0; i < FPW; ++i) dma16(src[i] + (size_t)gc * stride[i], &S.frag[wid + i * NW][0]);
-    if constexpr (!DOTS) dma4(psc + (size_t)min(g, slast) * sstride, &S.sc[64 * wid]);
+    for (int k = 0; k < L16; ++k) dma16s(sbase[k] + (size_t)gc * stride[k], loff[k], &S.frag[k * NW + wid][0]);
+    if constexpr (!DOTS) dma4s(wsbase + (size_t)min(g, G) * P.np, (uint32_t)lane * 4, &S.ws[64 * ww]);
+  };
+  auto issue_x = [&](int c) {  // once per XCH groups: addresses are recomputed here, not kept live
+    int ln;  // lane id, read here so that nothing derived from it stays live across the loop
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+    const int xr = ln / PPR, xp = (ln % PPR) ^ (xr % PPR);
+    const int g0 = XCH * c + 4 * xp;
+    const uint32_t off = 4u * (uint32_t)(g0 < G ? g0 : 0);  // pieces past the last group: in-bounds dummy, never read
+#pragma unroll
+    for (int k = 0; k < XPW; ++k) {
+      const int d = k * NW + wid;
+      const int r0 = min(m0 + RPD * d, P.m - 1);
+      const uint32_t row = (uint32_t)((min(m0 + RPD * d + xr, P.m - 1) - r0) * P.ldxs * 4);
+      dma16s(P.xs + (size_t)r0 * P.ldxs, row + off, &xc[c & 1].d[d][0]);
+    }
   };
 
   const int wm = wid / WN, wn = wid - (wid / WN) * WN;
-  const int fa = 2 * RT * wm;   // first A fragment of this wave
-  const int fbw = AF + 2 * CT * wn;  // first B fragment
+  const int fbw = AS + 2 * CT * wn;  // first B fragment of this wave
+  // A operand: lane reads row R = WR*wm + 32r + lane%32, chunk 2h + lane/32.
+  int aoff[RT][2];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int R = WR * wm + 32 * r + (lane & 31);
+      const int rr = R & 15, c = 2 * h + (lane >> 5);
+      aoff[r][h] = (R >> 4) * kFragBytes + 16 * (4 * rr + (c ^ swz(rr)));
+    }
+  // x scale of this lane's K=1 A row: RT == 2: row WR*wm + lane; RT == 1: row WR*wm + lane%32.
+  // Its address for group g: (xbx ^ 16*(gg/4)) + 4*(gg%4) + chunk buffer, with
+  // gg = g % XCH; xbase has its low 4 + log2(PPR) bits clear, so the XOR only
+  // swizzles the piece index.
+  const int xrow = WR * wm + (RT == 2 ? lane : (lane & 31));
+  const int xbase = (xrow / RPD) * kFragBytes + 16 * ((xrow % RPD) * PPR);
+  const int xbx = xbase + 16 * ((xrow % RPD) % PPR);
 
   v16i cinit;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) cinit[i] = CVT_VALU ? 0 : kMagicBits;
+  for (int i = 0; i < 16; ++i) cinit[i] = kMagicBits;
   v32f zero32;
 #pragma unroll
   for (int i = 0; i < 32; ++i) zero32[i] = 0.0f;
@@ -378,6 +456,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_linear_wide(Batch b) {
 #pragma unroll
   for (int j = 0; j < NP; ++j) s[j] = zero32;
 
+  if constexpr (!DOTS) issue_x(0);
 #pragma unroll
   for (int i = 0; i < STAGES - 1; ++i) {
     issue(stage(i), i);
@@ -392,21 +471,23 @@ __global__ __launch_bounds__(64 * WM * WN) void k_linear_wide(Batch b) {
       wait_vmcnt<LOADS * (STAGES - 2)>();
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      issue(stage((d + STAGES - 1) % STAGES), g + STAGES - 1);
+      const int gn = g + STAGES - 1;
+      if constexpr (!DOTS) {
+        if (gn % XCH == 0 && gn < G) issue_x(gn / XCH);
+      }
+      issue(stage((d + STAGES - 1) % STAGES), gn);
       __builtin_amdgcn_sched_barrier(0);
-      const v4i* fr = reinterpret_cast<const v4i*>(&cur.frag[0][0]);
+      const uint8_t* fr = &cur.frag[0][0];
       v4i af[RT][2], bf[CT][2];
 #pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        af[r][0] = fr[(fa + 2 * r) * 64 + lane];
-        af[r][1] = fr[(fa + 2 * r + 1) * 64 + lane];
-      }
+      for (int r = 0; r < RT; ++r)
 #pragma unroll
-      for (int j = 0; j < CT; ++j) {
-        bf[j][0] = fr[(fbw + 2 * j) * 64 + lane];
-        bf[j][1] = fr[(fbw + 2 * j + 1) * 64 + lane];
-      }
-      // dt[r][j]: dot tile of row tile r, column tile j (two MFMAs, K = 32 each).
+        for (int h = 0; h < 2; ++h) af[r][h] = *reinterpret_cast<const v4i*>(fr + aoff[r][h]);
+#pragma unroll
+      for (int j = 0; j < CT; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          bf[j][h] = *reinterpret_cast<const v4i*>(fr + (fbw + 2 * j + h) * kFragBytes + 16 * lane);
       v16i dt[RT][CT];
 #pragma unroll
       for (int r = 0; r < RT; ++r)
@@ -425,32 +506,18 @@ __global__ __launch_bounds__(64 * WM * WN) void k_linear_wide(Batch b) {
             for (int v = 0; v < 16; ++v) {
               const int row = m0 + WR * wm + 32 * r + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
               const int col = n0 + WC * wn + 32 * j + (lane & 31);
-              if (row < P.m && col < P.n)
-                P.dots[((size_t)row * P.n + col) * G + g] = dt[r][j][v] - (CVT_VALU ? 0 : kMagicBits);
+              if (row < P.m && col < P.n) P.dots[((size_t)row * P.n + col) * G + g] = dt[r][j][v] - kMagicBits;
             }
       } else {
+        const int gg = g % XCH;
+        const int xoff = (xbx ^ (16 * (gg >> 2))) + 4 * (gg & 3) + ((g / XCH) & 1) * (int)sizeof(XChunk);
+        const float x = *reinterpret_cast<const float*>(reinterpret_cast<const uint8_t*>(&xc[0]) + xoff);
 #pragma unroll
         for (int j = 0; j < NP; ++j) {
           const v16i& lo = RT == 2 ? dt[0][j] : dt[0][0];
           const v16i& hi = RT == 2 ? dt[1][j] : dt[0][1];
-          float x, w;
-          if constexpr (RT == 2) {
-            x = cur.sc[WR * wm + lane];
-            w = cur.sc[BM + WC * wn + 32 * j + (lane & 31)];
-          } else {
-            x = cur.sc[WR * wm + (lane & 31)];
-            w = cur.sc[BM + WC * wn + lane];
-          }
-          v32f dv;
-          if constexpr (CVT_VALU) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              dv[v] = (float)lo[v];
-              dv[16 + v] = (float)hi[v];
-            }
-          } else {
-            dv = mfma_k1(-kMagic, 1.0f, concat(lo, hi));
-          }
+          const float w = RT == 2 ? cur.ws[WC * wn + 32 * j + (lane & 31)] : cur.ws[WC * wn + lane];
+          const v32f dv = mfma_k1(-kMagic, 1.0f, concat(lo, hi));
           const v32f pv = mfma_k1(x, w, zero32);
           s[j] = s[j] + dv * pv;
         }
@@ -523,7 +590,7 @@ __global__ __launch_bounds__(256) void k_linear_skinny16(Batch b) {
 
   // A: lane l holds row r0 + l%16, bytes 16*(l/16) of the group.
   const int8_t* pa = P.q + (size_t)min(r0 + (lane & 15), P.m - 1) * P.ldq + 16 * (lane >> 4);
-  const float* pxs = P.xs + (size_t)min(r0 + 4 * (lane >> 4) + (lane & 3), P.m - 1) * G;  // K=1 A-lane row
+  const float* pxs = P.xs + (size_t)min(r0 + 4 * (lane >> 4) + (lane & 3), P.m - 1) * P.ldxs;  // K=1 A-lane row
   // B: lane l holds column c0 + l%16, bytes 16*(l/16): in the 32-row fragment
   // layout that is half l/32, lane (c0%32) + l%16 + 32*((l/16)&1).
   const uint8_t* pb = P.wt + ((size_t)(c0 / 32) * G * 2 + (lane >> 5)) * kFragBytes +
@@ -596,11 +663,11 @@ __global__ __launch_bounds__(256) void k_linear_skinny16(Batch b) {
 
 static unsigned blocks_for(long n, int per) { return (unsigned)((n + per - 1) / per); }
 
-hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, float* scales, uint32_t* nonfinite,
-                           hipStream_t s) {
+hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
+                           uint32_t* nonfinite, hipStream_t s) {
   const long waves = (long)rows * ((k + 255) / 256);
   if (waves == 0) return hipSuccess;
-  k_quantize<<<blocks_for(waves, 4), 256, 0, s>>>(x, rows, k, q, ldq, scales, nonfinite);
+  k_quantize<<<blocks_for(waves, 4), 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
   return hipGetLastError();
 }
 
@@ -618,6 +685,13 @@ hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipSt
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   k_export_scales<<<blocks_for((long)w->n * w->g, 256), 256, 0, s>>>(w->scales, w->n, w->g, w->np, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_pad_scales(const float* xs, int rows, int g, float* dst, int ld, hipStream_t s) {
+  const long n = (long)rows * ld;
+  if (n == 0) return hipSuccess;
+  k_pad_scales<<<blocks_for(n, 256), 256, 0, s>>>(xs, rows, g, dst, ld);
   return hipGetLastError();
 }
 
@@ -640,10 +714,10 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
     // total_waves counts blocks for the wide kernel
     constexpr int threads = 64 * DQ8_WIDE_WM * DQ8_WIDE_WN;
     if (dots)
-      k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_CVT_VALU, true>
+      k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_XCH, DQ8_WIDE_SWZ, true>
           <<<b.total_waves, threads, 0, s>>>(b);
     else
-      k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_CVT_VALU, false>
+      k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_XCH, DQ8_WIDE_SWZ, false>
           <<<b.total_waves, threads, 0, s>>>(b);
     return hipGetLastError();
   }
