@@ -127,11 +127,15 @@ int xcd_rows_split(int row_tiles, int col_tiles, size_t a_bytes, size_t b_bytes)
   return best;
 }
 
+// Kernel kind of a projection (see launch_linear).
+int kind_of(const dq8::Weights&, size_t m) { return m > 32 ? 0 : 1; }
+
 // Place a filled projection in a launch of the given kernel kind: its first
 // wave/block, column strips, XCD split and the launch's running total.
 void place_proj(dq8::Proj& p, int kind, dq8::Batch& b) {
   p.wave_begin = b.total_waves;
   p.xcd_gm = 0;
+  p.nseg = 1;
   if (kind == 0) {
     p.waves_n = p.np / dq8::wide_block_cols();
     const int row_tiles = (p.m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows();
@@ -139,7 +143,9 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b) {
     b.total_waves += p.waves_n * row_tiles;
   } else {
     p.waves_n = p.np / dq8::skinny_cols();
-    b.total_waves += p.waves_n * dq8::skinny_row_waves(p.m);
+    p.nseg = dq8::skinny_segments(p.g);
+    const int tiles = p.waves_n * dq8::skinny_row_waves(p.m), per_block = 4 / p.nseg;
+    b.total_waves += (tiles + per_block - 1) / per_block;
   }
 }
 
@@ -148,9 +154,9 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b) {
 // to G*64 bytes per row, into the context workspace.
 bool needs_pad(const dq8::Weights& w, const int8_t* q) { return w.k % kGroup != 0 || !aligned(q, 16); }
 size_t pad_bytes(const dq8::Weights& w, size_t m) { return (m * (size_t)w.g * kGroup + 255) / 256 * 256; }
-// The wide kernel loads x scales in 16-byte pieces of 4 groups: rows must be
+// The kernels load x scales in 16-byte pieces of 4 groups: rows must be
 // 16-byte aligned with a stride that is a multiple of 4 floats.  Otherwise they
-// are copied into the workspace with the stride rounded up.
+// are copied into the workspace with the stride rounded up (zero past G).
 int padded_groups(const dq8::Weights& w) { return (w.g + 3) / 4 * 4; }
 bool needs_xs_pad(const dq8::Weights& w, const float* xs) { return w.g % 4 != 0 || !aligned(xs, 16); }
 size_t xs_pad_bytes(const dq8::Weights& w, size_t m) {
@@ -173,21 +179,25 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
   for (size_t i = 0; i < count; ++i) {
     if (!items[i].m) continue;
     if (needs_pad(items[i].w->w, items[i].q)) need += pad_bytes(items[i].w->w, items[i].m);
-    if (!dots && items[i].m > 32 && needs_xs_pad(items[i].w->w, items[i].scales))
+    if (!dots && needs_xs_pad(items[i].w->w, items[i].scales))
       need += xs_pad_bytes(items[i].w->w, items[i].m);
   }
   if (need) {
     dq8_status st = ensure_work(ctx, need);
     if (st != DQ8_OK) return st;
   }
-  dq8::Batch batch[3];
+  dq8::Batch batch[2];
   for (dq8::Batch& b : batch) b.count = b.total_waves = 0;
   size_t offset = 0;
+  // Two passes: projections with long K (more than 32 groups) first, so their
+  // blocks start when the launch does instead of trailing the short ones.
+  for (int pass = 0; pass < 2; ++pass)
   for (size_t i = 0; i < count; ++i) {
     const dq8_linear_item& it = items[i];
     if (it.m == 0) continue;
     const dq8::Weights& w = it.w->w;
-    const int kind = it.m > 32 ? 0 : it.m <= 16 ? 1 : 2;
+    if ((w.g > 32) != (pass == 0)) continue;
+    const int kind = kind_of(w, it.m);
     dq8::Batch& b = batch[kind];
     if (b.count == dq8::kMaxBatch) {
       hipError_t e = dq8::launch_linear(b, kind, dots != nullptr, s);
@@ -207,7 +217,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     }
     const float* xs = it.scales;
     int ldxs = w.g;
-    if (!dots && kind == 0 && needs_xs_pad(w, it.scales)) {  // the dots kernels read no scales
+    if (!dots && needs_xs_pad(w, it.scales)) {  // the dots kernels read no scales
       float* dst = (float*)((char*)ctx->work + offset);
       ldxs = padded_groups(w);
       hipError_t e = dq8::launch_pad_scales(it.scales, (int)it.m, w.g, dst, ldxs, s);
@@ -219,7 +229,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     fill_proj(p, w, q, ldq, xs, ldxs, it.m, it.bias, it.out, dots, it.layout, it.epilogue);
     place_proj(p, kind, b);
   }
-  for (int kind = 0; kind < 3; ++kind) {
+  for (int kind = 0; kind < 2; ++kind) {
     if (batch[kind].count == 0) continue;
     hipError_t e = dq8::launch_linear(batch[kind], kind, dots != nullptr, s);
     if (e != hipSuccess) return from_hip(e);
@@ -416,7 +426,7 @@ dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, 
   dq8::Proj& p = b.p[0];
   fill_proj(p, w->w, q, (int)ldq, xs, ldxs, m, bias, out, nullptr, layout, epilogue);
   b.total_waves = 0;
-  const int kind = m > 32 ? 0 : m <= 16 ? 1 : 2;
+  const int kind = kind_of(w->w, m);
   place_proj(p, kind, b);
   return from_hip(dq8::launch_linear(b, kind, false, s));
 }

@@ -37,15 +37,16 @@ struct Proj {
   int m, ldq, ldxs, g, n, np;
   int epilogue;       // 0 write, 1 add, 2 swiglu
   int layout;         // 0 rows [M][N], 1 columns [N][M]
-  int wave_begin;     // first wave (skinny) or block (wide) of this projection in the launch
+  int wave_begin;     // first block of this projection in the launch
   int waves_n;        // column strips (skinny: skinny_cols() wide, wide: one block tile wide)
   int xcd_gm;         // wide: row bands of the per-XCD tile regions (1, 2, 4, 8), 0 = row-major order
+  int nseg;           // skinny: waves per 16x16 tile (1, 2, 4)
 };
 
 struct Batch {
   Proj p[kMaxBatch];
   int count;
-  int total_waves;  // waves (skinny) or blocks (wide) of the launch
+  int total_waves;  // blocks of the launch
 };
 
 // Kernel launchers (dq8_kernels.hip).  All return hipError_t of the launch.
@@ -56,12 +57,13 @@ hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int 
 hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipStream_t s);
 hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ldq, hipStream_t s);
 hipError_t launch_pad_scales(const float* xs, int rows, int g, float* dst, int ld, hipStream_t s);
-// Kind: 0 wide (M > 32), 1 skinny with M <= 16, 2 skinny with 16 < M <= 32.
-// dots selects the debug kernel.
+// Kind: 0 wide (M > 32), 1 skinny (M <= 32).  dots selects the debug kernel.
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s);
-// Columns per wave of the skinny kernel, and its waves per column strip for m rows.
+// Columns of a skinny tile, and the 16-row tiles of m rows.
 int skinny_cols();
 int skinny_row_waves(int m);
+// Waves per skinny tile for g groups (1, 2 or 4).
+int skinny_segments(int g);
 // Block tile of the wide kernel (rows, columns); kColPad is a multiple of the columns.
 int wide_block_rows();
 int wide_block_cols();

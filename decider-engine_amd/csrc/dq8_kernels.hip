@@ -260,6 +260,13 @@ __device__ __forceinline__ void dma4s(const void* base, uint32_t off, const void
                : "s"(lds_offset(lds)), "v"(off), "s"(base)
                : "memory");
 }
+// Block barrier for LDS data: this wave's LDS writes are complete, then
+// s_barrier.  Unlike __syncthreads() it does not wait for outstanding global
+// loads, so register prefetch rings keep their loads in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+}
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
@@ -553,16 +560,13 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 }
 
 // ---------------------------------------------------------------------------
-// Skinny projection kernel, 16 x 16 wave tiles (M <= 32).  Each wave owns one
-// 16-row tile x 16 columns and walks the groups one at a time:
-//   v_mfma_i32_16x16x64_i8 gives one group's dots for the tile (row
+// Skinny projection kernel (M <= 32), 16 x 16 tiles:
+//   v_mfma_i32_16x16x64_i8 gives one group's dots for a tile (row
 //   4*(l/16) + v, column l%16), C = the bias bits 0x4B400000;
 //   v_mfma_f32_4x4x1_16b_f32 with A = -12582912, B = 1 converts them exactly;
 //   the same instruction with A lane a = x of row 4*(a/16) + a%4 and B lane l =
 //   w of column l%16 is the product outer product in the same layout.
-// The row tiles of one 16-column strip are adjacent waves of a block, so the
-// strip's weights come from HBM once and from L1/L2 for the other row tiles.
-// Short dependency chains and many waves hide the memory latency.
+// Operands stream from memory through a register ring of DEPTH groups.
 struct Skinny16Frag {
   v4i a, b;
   float x, w;
@@ -575,38 +579,64 @@ __device__ __forceinline__ v4f mfma_k1_4(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
 }
 
+// Skinny projection (M <= 32), 16 x 16 tiles, with the groups of a tile
+// optionally interleaved over P.nseg waves (1, 2 or 4).  A block of 4 waves
+// holds 4 / nseg tiles; wave w works on tile w / nseg and takes the groups
+// g = j, j + nseg, j + 2*nseg, ... with j = w % nseg.
+//  * nseg == 1: the wave walks all groups and accumulates s itself.
+//  * nseg > 1: in round r the tile's waves compute t = dot * p for the groups
+//    r*nseg .. r*nseg + nseg - 1 (one each) and write them to LDS; after the
+//    block barrier the tile's first wave adds them in group order.  Every
+//    output is the left-to-right sum of one sequential pass, with nseg times
+//    the loads in flight per tile and no t's held in registers.
+// The two row tiles of a strip (16 < M <= 32) sit in one block, or, at one
+// tile per block, in blocks i and i+8, which the round-robin dispatch places
+// on one XCD: the strip's weights then come from HBM once.
 template <int DEPTH, bool DOTS>
-__global__ __launch_bounds__(256) void k_linear_skinny16(Batch b) {
+__global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
+  __shared__ v4f tb[2][4][64];  // t of the current / previous round, by wave, per lane
   const int lane = threadIdx.x & 63;
-  const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (wave >= b.total_waves) return;
-  const Proj P = b.p[find_proj(b, wave)];
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int blk = blockIdx.x;
+  const Proj P = b.p[find_proj(b, blk)];
   const int rtiles = (P.m + 15) >> 4;
-  const int w_local = wave - P.wave_begin;
-  const int nt = w_local / rtiles;  // 16-column strip
-  const int r0 = (w_local - nt * rtiles) * 16;
+  const int nseg = P.nseg, tpb = 4 / nseg;
+  const int tiles = P.waves_n * rtiles;
+  const int local = blk - P.wave_begin;
+  const int sidx = wid % nseg, tib = wid / nseg;
+  const int tile = local * tpb + tib;
+  int nt, rt;
+  if (rtiles == 2 && tpb == 1) {
+    nt = 8 * (local >> 4) + (local & 7);
+    rt = (local >> 3) & 1;
+  } else {
+    nt = tile / rtiles;
+    rt = tile - nt * rtiles;
+  }
+  const bool live = tile < tiles;  // the last block of a projection may hold fewer tiles
+  if (!live) nt = rt = 0;          // any valid tile: loads stay in bounds, nothing is stored
+  const int r0 = rt * 16;
   const int c0 = nt * 16;
   const int G = P.g;
+  const int rounds = (G + nseg - 1) / nseg;  // uniform over the block
 
-  // A: lane l holds row r0 + l%16, bytes 16*(l/16) of the group.
   const int8_t* pa = P.q + (size_t)min(r0 + (lane & 15), P.m - 1) * P.ldq + 16 * (lane >> 4);
-  const float* pxs = P.xs + (size_t)min(r0 + 4 * (lane >> 4) + (lane & 3), P.m - 1) * P.ldxs;  // K=1 A-lane row
-  // B: lane l holds column c0 + l%16, bytes 16*(l/16): in the 32-row fragment
-  // layout that is half l/32, lane (c0%32) + l%16 + 32*((l/16)&1).
+  const float* pxs = P.xs + (size_t)min(r0 + 4 * (lane >> 4) + (lane & 3), P.m - 1) * P.ldxs;
   const uint8_t* pb = P.wt + ((size_t)(c0 / 32) * G * 2 + (lane >> 5)) * kFragBytes +
                       ((c0 & 31) + (lane & 15) + 32 * ((lane >> 4) & 1)) * 16;
   const float* pws = P.wst + c0 + (lane & 15);
 
-  auto load = [&](Skinny16Frag& f, int g) {
-    const int gc = min(g, G - 1);
+  // Slot of round r: group r*nseg + sidx (clamped: prefetches past the end
+  // read a valid group and are never used).
+  auto load = [&](Skinny16Frag& f, int r) {
+    const int gc = min(r * nseg + sidx, G - 1);
     f.a = load16(pa + gc * kGroup);
     f.b = load16(pb + (size_t)gc * 2 * kFragBytes);
     if constexpr (!DOTS) {
       f.x = pxs[gc];
-      f.w = pws[(size_t)min(g, G) * P.np];  // row G of the w scales is zero
+      f.w = pws[(size_t)gc * P.np];
     }
   };
-
   v4i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
   const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
   v4f s = zero4;
@@ -617,20 +647,23 @@ __global__ __launch_bounds__(256) void k_linear_skinny16(Batch b) {
     load(ring[d], d);
     __builtin_amdgcn_sched_barrier(0);
   }
-  for (int g0 = 0; g0 < G; g0 += DEPTH) {
+  for (int r0_ = 0; r0_ < rounds; r0_ += DEPTH) {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      const int g = g0 + d;
+      const int r = r0_ + d;
+      if (r >= rounds) break;  // uniform over the block
+      const int g = r * nseg + sidx;
+      const bool has = live && g < G;
       const Skinny16Frag& c = ring[d];
       const v4i dd = mfma_i8_16(c.a, c.b, magic);
       v4f pv;
       if constexpr (!DOTS) pv = mfma_k1_4(c.x, c.w, zero4);
       // Refill the slot once every operand of it is consumed.
       __builtin_amdgcn_sched_barrier(0);
-      load(ring[d], g + DEPTH);
+      load(ring[d], r + DEPTH);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (DOTS) {
-        if (g < G) {
+        if (has) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int row = r0 + 4 * (lane >> 4) + v;
@@ -640,23 +673,41 @@ __global__ __launch_bounds__(256) void k_linear_skinny16(Batch b) {
         }
       } else {
         const v4f dv = mfma_k1_4(-kMagic, 1.0f, __builtin_bit_cast(v4f, dd));
-        s = s + dv * pv;
+        const v4f t = dv * pv;
+        if (nseg == 1) {
+          s = s + t;
+        } else {
+          // Round r's t's go to buffer r % 2; the first wave of the tile adds
+          // them after the barrier.  Buffer r % 2 is written again in round
+          // r + 2, after the barrier of round r + 1, by which time the adds
+          // of round r are done.
+          if (has) tb[r & 1][wid][lane] = t;
+          lds_barrier();
+          if (sidx == 0) {
+            const int n = min(nseg, G - r * nseg);
+            for (int j = 0; j < n; ++j) s = s + tb[r & 1][tib * nseg + j][lane];
+          }
+        }
       }
     }
   }
   if constexpr (!DOTS) {
-    const int col = c0 + (lane & 15);
-    const float bias = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
-    int rows[4], cols[4];
-    float y[4];
+    if (live && sidx == 0) {
+      const int col = c0 + (lane & 15);
+      const float bias = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
+      int rows[4], cols[4];
+      float y[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      rows[v] = r0 + 4 * (lane >> 4) + v;
-      cols[v] = col;
-      y[v] = s[v] + bias;
+      for (int v = 0; v < 4; ++v) {
+        rows[v] = r0 + 4 * (lane >> 4) + v;
+        cols[v] = col;
+        y[v] = s[v] + bias;
+      }
+      store_tile(P, rows, cols, y);
     }
-    store_tile(P, rows, cols, y);
   }
+  // drain the prefetches past the end before the wave exits
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 }  // namespace
@@ -700,11 +751,17 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
   return hipGetLastError();
 }
 
-#ifndef DQ8_SKINNY16_DEPTH
-#define DQ8_SKINNY16_DEPTH 4
+#ifndef DQ8_SKINNY_DEPTH
+#define DQ8_SKINNY_DEPTH 4
 #endif
 int skinny_cols() { return 16; }
+// Waves per skinny tile: projections with more than DQ8_SKINNY_SPLIT groups
+// interleave each tile's groups over 2 (up to twice that) or 4 waves.
+#ifndef DQ8_SKINNY_SPLIT
+#define DQ8_SKINNY_SPLIT 32
+#endif
 int skinny_row_waves(int m) { return (m + 15) / 16; }
+int skinny_segments(int g) { return g <= DQ8_SKINNY_SPLIT ? 1 : g <= 2 * DQ8_SKINNY_SPLIT ? 2 : 4; }
 int wide_block_rows() { return 32 * DQ8_WIDE_RT * DQ8_WIDE_WM; }
 int wide_block_cols() { return 32 * DQ8_WIDE_CT * DQ8_WIDE_WN; }
 
@@ -721,9 +778,9 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
           <<<b.total_waves, threads, 0, s>>>(b);
     return hipGetLastError();
   }
-  const unsigned blocks = blocks_for(b.total_waves, 4);
-  if (dots) k_linear_skinny16<DQ8_SKINNY16_DEPTH, true><<<blocks, 256, 0, s>>>(b);
-  else k_linear_skinny16<DQ8_SKINNY16_DEPTH, false><<<blocks, 256, 0, s>>>(b);
+  // total_waves counts blocks of 4 waves for the skinny kernel
+  if (dots) k_linear_skinny<DQ8_SKINNY_DEPTH, true><<<b.total_waves, 256, 0, s>>>(b);
+  else k_linear_skinny<DQ8_SKINNY_DEPTH, false><<<b.total_waves, 256, 0, s>>>(b);
   return hipGetLastError();
 }
 
