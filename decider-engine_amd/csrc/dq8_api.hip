@@ -128,7 +128,7 @@ int xcd_rows_split(int row_tiles, int col_tiles, size_t a_bytes, size_t b_bytes)
 }
 
 // Kernel kind of a projection (see launch_linear).
-int kind_of(const dq8::Weights&, size_t m) { return m > 32 ? 0 : 1; }
+int kind_of(const dq8::Weights&, size_t m) { return m > 32 ? 0 : m > 16 ? 2 : 1; }
 
 // Place a filled projection in a launch of the given kernel kind: its first
 // wave/block, column strips, XCD split and the launch's running total.
@@ -142,10 +142,10 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b) {
     p.xcd_gm = xcd_rows_split(row_tiles, p.waves_n, (size_t)p.m * p.g, (size_t)p.n * p.g);
     b.total_waves += p.waves_n * row_tiles;
   } else {
-    p.waves_n = p.np / dq8::skinny_cols();
+    p.waves_n = (p.n + dq8::skinny_cols(p.g) - 1) / dq8::skinny_cols(p.g);
     p.nseg = dq8::skinny_segments(p.g);
-    const int tiles = p.waves_n * dq8::skinny_row_waves(p.m), per_block = 4 / p.nseg;
-    b.total_waves += (tiles + per_block - 1) / per_block;
+    const int per_block = 4 / p.nseg;
+    b.total_waves += (p.waves_n + per_block - 1) / per_block;
   }
 }
 
@@ -186,7 +186,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     dq8_status st = ensure_work(ctx, need);
     if (st != DQ8_OK) return st;
   }
-  dq8::Batch batch[2];
+  dq8::Batch batch[dq8::kKinds];
   for (dq8::Batch& b : batch) b.count = b.total_waves = 0;
   size_t offset = 0;
   // Two passes: projections with long K (more than 32 groups) first, so their
@@ -229,7 +229,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     fill_proj(p, w, q, ldq, xs, ldxs, it.m, it.bias, it.out, dots, it.layout, it.epilogue);
     place_proj(p, kind, b);
   }
-  for (int kind = 0; kind < 2; ++kind) {
+  for (int kind = 0; kind < dq8::kKinds; ++kind) {
     if (batch[kind].count == 0) continue;
     hipError_t e = dq8::launch_linear(batch[kind], kind, dots != nullptr, s);
     if (e != hipSuccess) return from_hip(e);

@@ -38,9 +38,9 @@ struct Proj {
   int epilogue;       // 0 write, 1 add, 2 swiglu
   int layout;         // 0 rows [M][N], 1 columns [N][M]
   int wave_begin;     // first block of this projection in the launch
-  int waves_n;        // column strips (skinny: skinny_cols() wide, wide: one block tile wide)
+  int waves_n;        // column strips (skinny: skinny_cols(g) wide, wide: one block tile wide)
   int xcd_gm;         // wide: row bands of the per-XCD tile regions (1, 2, 4, 8), 0 = row-major order
-  int nseg;           // skinny: waves per 16x16 tile (1, 2, 4)
+  int nseg;           // skinny: waves per strip (1 or 4)
 };
 
 struct Batch {
@@ -57,12 +57,13 @@ hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int 
 hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipStream_t s);
 hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ldq, hipStream_t s);
 hipError_t launch_pad_scales(const float* xs, int rows, int g, float* dst, int ld, hipStream_t s);
-// Kind: 0 wide (M > 32), 1 skinny (M <= 32).  dots selects the debug kernel.
+// Kind: 0 wide (M > 32), 1 skinny (M <= 16), 2 skinny (16 < M <= 32).  dots
+// selects the debug kernel.
+constexpr int kKinds = 3;
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s);
-// Columns of a skinny tile, and the 16-row tiles of m rows.
-int skinny_cols();
-int skinny_row_waves(int m);
-// Waves per skinny tile for g groups (1, 2 or 4).
+// Columns of a skinny strip for g groups (all rows), and the waves that share
+// a strip's groups (1 or 4).
+int skinny_cols(int g);
 int skinny_segments(int g);
 // Block tile of the wide kernel (rows, columns); kColPad is a multiple of the columns.
 int wide_block_rows();

@@ -560,18 +560,34 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 }
 
 // ---------------------------------------------------------------------------
-// Skinny projection kernel (M <= 32), 16 x 16 tiles:
-//   v_mfma_i32_16x16x64_i8 gives one group's dots for a tile (row
+// Skinny projection kernel (M <= 32).  Per group and 16 x 16 tile:
+//   v_mfma_i32_16x16x64_i8 gives the group's dots (lane l, element v: row
 //   4*(l/16) + v, column l%16), C = the bias bits 0x4B400000;
 //   v_mfma_f32_4x4x1_16b_f32 with A = -12582912, B = 1 converts them exactly;
 //   the same instruction with A lane a = x of row 4*(a/16) + a%4 and B lane l =
 //   w of column l%16 is the product outer product in the same layout.
-// Operands stream from memory through a register ring of DEPTH groups.
-struct Skinny16Frag {
-  v4i a, b;
-  float x, w;
-};
-
+//
+// The kernel is a weight stream.  Its speed is set by the weight bytes in
+// flight (HBM latency under load is microseconds), so every wave keeps a deep
+// register ring of weight fragments and w scales, and a wave covers all rows
+// of its strip of 16*CT columns (each weight byte is loaded once):
+//  * short K (G <= 32): the block first loads its whole activation (16*RT rows
+//    x G*64 bytes, at most 64 KB) and x scales into LDS; then the waves run
+//    with no barriers.  Activation bytes land by direct loads of 8 rows x 128
+//    bytes (two groups; 8 whole cache lines per load): lane l fetches row l/8,
+//    16-byte chunk (l%8) ^ (l/8) and lands at slot l, so the MFMA operand
+//    reads are free of bank conflicts.
+//  * long K (G > 32): a strip's groups are interleaved over NSEG = 2 or 4
+//    waves (wave sidx takes the groups g with g % NSEG == sidx), so a strip
+//    has NSEG rings in flight.  Activation fragments join the register ring;
+//    x scales come through LDS in chunks of 8 steps.  Per step every wave
+//    posts its t's to LDS and, after a barrier, the strip's first wave adds
+//    them in group order: every output is still one left-to-right sum.
+// x scales in LDS: [row][piece of 4 groups] in 16-byte pieces, loaded 64
+// pieces per direct load (lane l: row l/XP, piece (l%XP) ^ (row%XP), XP pieces
+// per row) and read back with the same XOR.  Rows past M repeat row M-1 and
+// loads past the last group repeat the last one: every load stays in bounds;
+// no output of such a row or group is stored.
 __device__ __forceinline__ v4i mfma_i8_16(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
@@ -579,137 +595,350 @@ __device__ __forceinline__ v4f mfma_k1_4(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
 }
 
-// Skinny projection (M <= 32), 16 x 16 tiles, with the groups of a tile
-// optionally interleaved over P.nseg waves (1, 2 or 4).  A block of 4 waves
-// holds 4 / nseg tiles; wave w works on tile w / nseg and takes the groups
-// g = j, j + nseg, j + 2*nseg, ... with j = w % nseg.
-//  * nseg == 1: the wave walks all groups and accumulates s itself.
-//  * nseg > 1: in round r the tile's waves compute t = dot * p for the groups
-//    r*nseg .. r*nseg + nseg - 1 (one each) and write them to LDS; after the
-//    block barrier the tile's first wave adds them in group order.  Every
-//    output is the left-to-right sum of one sequential pass, with nseg times
-//    the loads in flight per tile and no t's held in registers.
-// The two row tiles of a strip (16 < M <= 32) sit in one block, or, at one
-// tile per block, in blocks i and i+8, which the round-robin dispatch places
-// on one XCD: the strip's weights then come from HBM once.
-template <int DEPTH, bool DOTS>
-__global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
-  __shared__ v4f tb[2][4][64];  // t of the current / previous round, by wave, per lane
-  const int lane = threadIdx.x & 63;
-  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int blk = blockIdx.x;
-  const Proj P = b.p[find_proj(b, blk)];
-  const int rtiles = (P.m + 15) >> 4;
-  const int nseg = P.nseg, tpb = 4 / nseg;
-  const int tiles = P.waves_n * rtiles;
-  const int local = blk - P.wave_begin;
-  const int sidx = wid % nseg, tib = wid / nseg;
-  const int tile = local * tpb + tib;
-  int nt, rt;
-  if (rtiles == 2 && tpb == 1) {
-    nt = 8 * (local >> 4) + (local & 7);
-    rt = (local >> 3) & 1;
-  } else {
-    nt = tile / rtiles;
-    rt = tile - nt * rtiles;
-  }
-  const bool live = tile < tiles;  // the last block of a projection may hold fewer tiles
-  if (!live) nt = rt = 0;          // any valid tile: loads stay in bounds, nothing is stored
-  const int r0 = rt * 16;
-  const int c0 = nt * 16;
-  const int G = P.g;
-  const int rounds = (G + nseg - 1) / nseg;  // uniform over the block
+// LDS bytes of the skinny kernel: the short-K preload (16 steps of activation
+// plus 32 groups of x scales) or the long-K x chunks and posted t's (ctl
+// column tiles per long-K wave).
+constexpr int skinny_lds_bytes(int rt, int ctl) {
+  const int short_k = 16 * rt * 2 * kFragBytes + 16 * rt * 8 * 16;
+  const int long_k = 2 * 16 * rt * 8 * 16 + 2 * 4 * rt * ctl * kFragBytes;
+  return short_k > long_k ? short_k : long_k;
+}
 
-  const int8_t* pa = P.q + (size_t)min(r0 + (lane & 15), P.m - 1) * P.ldq + 16 * (lane >> 4);
-  const float* pxs = P.xs + (size_t)min(r0 + 4 * (lane >> 4) + (lane & 3), P.m - 1) * P.ldxs;
-  const uint8_t* pb = P.wt + ((size_t)(c0 / 32) * G * 2 + (lane >> 5)) * kFragBytes +
-                      ((c0 & 31) + (lane & 15) + 32 * ((lane >> 4) & 1)) * 16;
-  const float* pws = P.wst + c0 + (lane & 15);
+// Byte offset in an x chunk of XP pieces per row of (row r, group gg of the chunk).
+template <int XP>
+__device__ __forceinline__ int x_slot(int r, int gg) {
+  return 16 * (r * XP + ((gg >> 2) ^ (r % XP))) + 4 * (gg & 3);
+}
 
-  // Slot of round r: group r*nseg + sidx (clamped: prefetches past the end
-  // read a valid group and are never used).
-  auto load = [&](Skinny16Frag& f, int r) {
-    const int gc = min(r * nseg + sidx, G - 1);
-    f.a = load16(pa + gc * kGroup);
-    f.b = load16(pb + (size_t)gc * 2 * kFragBytes);
-    if constexpr (!DOTS) {
-      f.x = pxs[gc];
-      f.w = pws[(size_t)gc * P.np];
+// Direct loads of x chunk c (XP pieces of 4 groups per row, ROWS rows) into
+// dst: this wave's share of the ROWS*XP/64 loads.  Needs 16-byte aligned rows
+// of ldxs % 4 == 0 floats.
+template <int ROWS, int XP>
+__device__ __forceinline__ void issue_x_chunk(const Proj& P, int c, int wid, uint8_t* dst) {
+  constexpr int LOADS = (ROWS * XP + 63) / 64;
+  const int last_piece = (P.g + 3) / 4 - 1;
+  int ln;  // lane id, read here so that nothing derived from it stays live
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+#pragma unroll
+  for (int k = 0; k < (LOADS + 3) / 4; ++k) {
+    const int i = wid + 4 * k;
+    if (i < LOADS) {
+      const int e = 64 * i + ln;
+      const int r = e / XP, pc = (e % XP) ^ (r % XP);
+      const int gp = min(c * XP + pc, last_piece);
+      const uint32_t off = (uint32_t)(min(r, P.m - 1) * P.ldxs + 4 * gp) * 4u;
+      dma16s(P.xs, off, dst + i * kFragBytes);
     }
-  };
-  v4i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
-  const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  v4f s = zero4;
-
-  Skinny16Frag ring[DEPTH];
-#pragma unroll
-  for (int d = 0; d < DEPTH; ++d) {
-    load(ring[d], d);
-    __builtin_amdgcn_sched_barrier(0);
   }
-  for (int r0_ = 0; r0_ < rounds; r0_ += DEPTH) {
+}
+
+// y = s + bias, or s + 0.0f without a bias (tensor.rs:437), stored by the epilogue.
+template <int RT, int CT>
+__device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, const v4f (&s)[RT * CT]) {
+  constexpr int E = 4 * RT * CT;
+  int rows[E], cols[E];
+  float y[E];
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int r = r0_ + d;
-      if (r >= rounds) break;  // uniform over the block
-      const int g = r * nseg + sidx;
-      const bool has = live && g < G;
-      const Skinny16Frag& c = ring[d];
-      const v4i dd = mfma_i8_16(c.a, c.b, magic);
-      v4f pv;
-      if constexpr (!DOTS) pv = mfma_k1_4(c.x, c.w, zero4);
-      // Refill the slot once every operand of it is consumed.
-      __builtin_amdgcn_sched_barrier(0);
-      load(ring[d], r + DEPTH);
-      __builtin_amdgcn_sched_barrier(0);
+  for (int ct = 0; ct < CT; ++ct) {
+    const int col = c0 + 16 * ct + (lane & 15);
+    const float bias = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int e = 4 * (rt * CT + ct) + v;
+        rows[e] = 16 * rt + 4 * (lane >> 4) + v;
+        cols[e] = col;
+        y[e] = s[rt * CT + ct][v] + bias;
+      }
+  }
+  store_tile(P, rows, cols, y);
+}
+
+// One group of a wave's tiles: dots (exported when DOTS) or t = dot * p.
+template <int RT, int CT, bool DOTS>
+__device__ __forceinline__ void skinny_group(const Proj& P, int c0, int lane, bool store, int g, const v4i (&a)[RT],
+                                             const v4i (&bw)[CT], const float (&x)[RT], const float (&ws)[CT],
+                                             v4f (&t)[RT * CT]) {
+  const v4i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+  const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      const v4i dd = mfma_i8_16(a[rt], bw[ct], magic);
       if constexpr (DOTS) {
-        if (has) {
+        if (store) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const int row = r0 + 4 * (lane >> 4) + v;
-            const int col = c0 + (lane & 15);
-            if (row < P.m && col < P.n) P.dots[((size_t)row * P.n + col) * G + g] = dd[v] - kMagicBits;
+            const int row = 16 * rt + 4 * (lane >> 4) + v;
+            const int col = c0 + 16 * ct + (lane & 15);
+            if (row < P.m && col < P.n) P.dots[((size_t)row * P.n + col) * P.g + g] = dd[v] - kMagicBits;
           }
         }
       } else {
         const v4f dv = mfma_k1_4(-kMagic, 1.0f, __builtin_bit_cast(v4f, dd));
-        const v4f t = dv * pv;
-        if (nseg == 1) {
-          s = s + t;
-        } else {
-          // Round r's t's go to buffer r % 2; the first wave of the tile adds
-          // them after the barrier.  Buffer r % 2 is written again in round
-          // r + 2, after the barrier of round r + 1, by which time the adds
-          // of round r are done.
-          if (has) tb[r & 1][wid][lane] = t;
-          lds_barrier();
-          if (sidx == 0) {
-            const int n = min(nseg, G - r * nseg);
-            for (int j = 0; j < n; ++j) s = s + tb[r & 1][tib * nseg + j][lane];
-          }
+        const v4f pv = mfma_k1_4(x[rt], ws[ct], zero4);
+        t[rt * CT + ct] = dv * pv;
+      }
+    }
+}
+
+// Short K (G <= 32): 4 strips per block, one wave each, 2 groups per step.
+template <int RT, int CT, int DB, bool DOTS>
+__device__ __forceinline__ void skinny_short(const Proj& P, int local, int wid, int lane, uint8_t* lds) {
+  constexpr int ROWS = 16 * RT;
+  constexpr int STEP_A = RT * 2 * kFragBytes;  // activation bytes of one step (8-row units)
+  constexpr int OPS = 2 * CT * (DOTS ? 1 : 2);  // ring loads per step
+  static_assert(DB >= 2 && (DB - 1) * OPS <= 63, "ring depth");
+  uint8_t* xl = lds + 16 * STEP_A;  // x scales: one chunk of 32 groups (8 pieces per row)
+  const int strip = local * 4 + wid;
+  const bool live = strip < P.waves_n;  // the last block of a projection may hold fewer strips
+  const int c0 = (live ? strip : 0) * 16 * CT;
+  const int G = P.g;
+  const int steps = (G + 1) >> 1;
+
+  const uint8_t* pb[CT];
+  const float* pw[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int cc = c0 + 16 * ct;
+    pb[ct] = P.wt + ((size_t)(cc >> 5) * G * 2 + (lane >> 5)) * kFragBytes +
+             ((cc & 31) + (lane & 15) + 32 * ((lane >> 4) & 1)) * 16;
+    pw[ct] = P.wst + cc + (lane & 15);
+  }
+  v4i bq[DB][2][CT];
+  float wq[DB][2][CT];
+  auto issue = [&](v4i (&bs)[2][CT], float (&ws)[2][CT], int j) {
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      const int g = min(2 * j + gi, G - 1);
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        bs[gi][ct] = load16(pb[ct] + (size_t)g * 2 * kFragBytes);
+        if constexpr (!DOTS) ws[gi][ct] = pw[ct][(size_t)g * P.np];
+      }
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < DB - 1; ++d) {
+    issue(bq[d], wq[d], min(d, steps - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // Preload: activation unit u = 2*RT*j + o (step j, row octet o), then the x chunk.
+  {
+    const int units = steps * 2 * RT;
+    const int sr = lane >> 3, c8 = (lane & 7) ^ (lane >> 3);
+    for (int u = wid; u < units; u += 4) {
+      const int j = u / (2 * RT), o = u - j * 2 * RT;
+      const int grp = min(2 * j + (c8 >> 2), G - 1);
+      const uint32_t off = (uint32_t)(min(8 * o + sr, P.m - 1) * P.ldq + 64 * grp + 16 * (c8 & 3));
+      dma16s(P.q, off, lds + j * STEP_A + o * kFragBytes);
+    }
+    if constexpr (!DOTS) issue_x_chunk<ROWS, 8>(P, 0, wid, xl);
+  }
+  wait_vmcnt<0>();
+  lds_barrier();
+
+  int aoff[RT][2];  // [row tile][group parity]: row 16rt + l%16, chunk 4*parity + l/16
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int par = 0; par < 2; ++par) {
+      const int r = 16 * rt + (lane & 15), c8 = 4 * par + (lane >> 4);
+      aoff[rt][par] = (r >> 3) * kFragBytes + 16 * (8 * (r & 7) + (c8 ^ (r & 7)));
+    }
+  int xr[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) xr[rt] = 16 * rt + 4 * (lane >> 4) + (lane & 3);
+
+  const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  v4f s[RT * CT];
+#pragma unroll
+  for (int k = 0; k < RT * CT; ++k) s[k] = zero4;
+  // Step j from ring slot d (a constant after unrolling).  Every slot is
+  // consumed on every path (the odd last group is computed on a clamped copy
+  // and dropped), and the ring loop has no early exit: the compiler's load
+  // waits then stay exact instead of draining the ring at the loop header.
+  auto step = [&](int j, int d) __attribute__((always_inline)) {
+    const int nd = (d + DB - 1) % DB;
+    issue(bq[nd], wq[nd], min(j + DB - 1, steps - 1));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int gi = 0; gi < 2; ++gi) {
+      const int g = 2 * j + gi;
+      const int gx = min(g, G - 1);
+      v4i a[RT];
+      float x[RT];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        a[rt] = *reinterpret_cast<const v4i*>(lds + j * STEP_A + aoff[rt][gi]);
+        if constexpr (!DOTS) x[rt] = *reinterpret_cast<const float*>(xl + x_slot<8>(xr[rt], gx));
+      }
+      v4f t[RT * CT];
+      skinny_group<RT, CT, DOTS>(P, c0, lane, live && g < G, g, a, bq[d][gi], x, wq[d][gi], t);
+      if constexpr (!DOTS) {
+        if (g < G) {  // uniform
+#pragma unroll
+          for (int k = 0; k < RT * CT; ++k) s[k] = s[k] + t[k];
         }
       }
     }
-  }
-  if constexpr (!DOTS) {
-    if (live && sidx == 0) {
-      const int col = c0 + (lane & 15);
-      const float bias = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
-      int rows[4], cols[4];
-      float y[4];
+  };
+  int j0 = 0;
+  for (; j0 + DB <= steps; j0 += DB) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        rows[v] = r0 + 4 * (lane >> 4) + v;
-        cols[v] = col;
-        y[v] = s[v] + bias;
-      }
-      store_tile(P, rows, cols, y);
-    }
+    for (int d = 0; d < DB; ++d) step(j0 + d, d);
   }
-  // drain the prefetches past the end before the wave exits
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int d = 0; d < DB - 1; ++d)
+    if (j0 + d < steps) step(j0 + d, d);
+  wait_vmcnt<0>();  // the clamped loads past the end
+  if constexpr (!DOTS)
+    if (live) skinny_store<RT, CT>(P, c0, lane, s);
 }
 
+// Long K (G > 32): 4/NSEG strips per block, NSEG waves each, one group per wave and step.
+template <int RT, int CT, int DB, int NSEG, bool DOTS>
+__device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, int lane, uint8_t* lds) {
+  constexpr int ROWS = 16 * RT, NT = RT * CT, TPB = 4 / NSEG;
+  constexpr int XP = 2 * NSEG;                 // x pieces per row of a chunk of 8 steps (8*NSEG groups)
+  constexpr int XBYTES = ROWS * XP * 16;
+  constexpr int OPS = CT * (DOTS ? 1 : 2) + RT;  // ring loads per step
+  static_assert(DB >= 2 && (DB - 1) * OPS <= 63 && DB <= 10, "ring depth");
+  constexpr int WAIT_X0 = (DB - 1) * OPS, WAIT_X = 8 * OPS < 63 ? 8 * OPS : 63;
+  uint8_t* xl = lds;  // x chunks, double-buffered
+  v4f(*tb)[4][NT][64] = reinterpret_cast<v4f(*)[4][NT][64]>(lds + 2 * XBYTES);  // posted t's
+  const int sidx = wid % NSEG, tib = wid / NSEG;
+  const int strip = local * TPB + tib;
+  const bool live = strip < P.waves_n;
+  const int c0 = (live ? strip : 0) * 16 * CT;
+  const int G = P.g;
+  const int steps = (G + NSEG - 1) / NSEG;
+  const int chunks = (G + 8 * NSEG - 1) / (8 * NSEG);
+
+  const int8_t* pa[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) pa[rt] = P.q + (size_t)min(16 * rt + (lane & 15), P.m - 1) * P.ldq + 16 * (lane >> 4);
+  const uint8_t* pb[CT];
+  const float* pw[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int cc = c0 + 16 * ct;
+    pb[ct] = P.wt + ((size_t)(cc >> 5) * G * 2 + (lane >> 5)) * kFragBytes +
+             ((cc & 31) + (lane & 15) + 32 * ((lane >> 4) & 1)) * 16;
+    pw[ct] = P.wst + cc + (lane & 15);
+  }
+  v4i aq[DB][RT], bq[DB][CT];
+  float wq[DB][CT];
+  auto issue = [&](v4i (&as)[RT], v4i (&bs)[CT], float (&ws)[CT], int j) {
+    const int g = min(j * NSEG + sidx, G - 1);
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      bs[ct] = load16(pb[ct] + (size_t)g * 2 * kFragBytes);
+      if constexpr (!DOTS) ws[ct] = pw[ct][(size_t)g * P.np];
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) as[rt] = load16(pa[rt] + g * kGroup);
+  };
+  int xr[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) xr[rt] = 16 * rt + 4 * (lane >> 4) + (lane & 3);
+  const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  v4f s[NT];
+#pragma unroll
+  for (int k = 0; k < NT; ++k) s[k] = zero4;
+  auto add_posted = [&](int j) {  // first wave of a strip: the step's t's in group order
+    if (sidx == 0) {
+      v4f tp[NSEG][NT];  // all reads first, then the adds in order
+#pragma unroll
+      for (int i = 0; i < NSEG; ++i)
+#pragma unroll
+        for (int k = 0; k < NT; ++k) tp[i][k] = tb[j & 1][tib * NSEG + i][k][lane];
+#pragma unroll
+      for (int i = 0; i < NSEG; ++i)
+        if (j * NSEG + i < G) {  // uniform: groups past G in the last step are not added
+#pragma unroll
+          for (int k = 0; k < NT; ++k) s[k] = s[k] + tp[i][k];
+        }
+    }
+  };
+
+  if constexpr (!DOTS) issue_x_chunk<ROWS, XP>(P, 0, wid, xl);
+#pragma unroll
+  for (int d = 0; d < DB - 1; ++d) {
+    issue(aq[d], bq[d], wq[d], min(d, steps - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // Step j from ring slot d (a constant after unrolling); as in the short-K
+  // loop, every slot is consumed on every path and the ring loop has no early
+  // exit.  Groups past G (the last step) are computed on clamped copies; their
+  // t's are posted but not added.
+  auto step = [&](int j, int d) __attribute__((always_inline)) {
+    const bool chunk_start = (j & 7) == 0;
+    // x chunk j/8 was issued 8 steps ago (chunk 0: before the prologue); the
+    // waits let through only the ring loads issued after it.
+    if constexpr (!DOTS) {
+      if (chunk_start) {
+        if (j == 0) wait_vmcnt<WAIT_X0>();
+        else wait_vmcnt<WAIT_X>();
+      }
+    }
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!DOTS) {
+      if (chunk_start && (j >> 3) + 1 < chunks)
+        issue_x_chunk<ROWS, XP>(P, (j >> 3) + 1, wid, xl + (((j >> 3) + 1) & 1) * XBYTES);
+    }
+    const int nd = (d + DB - 1) % DB;
+    issue(aq[nd], bq[nd], wq[nd], min(j + DB - 1, steps - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (!DOTS)
+      if (j > 0) add_posted(j - 1);
+    const int g = j * NSEG + sidx;
+    float x[RT];
+    if constexpr (!DOTS) {
+      const uint8_t* xc = xl + ((j >> 3) & 1) * XBYTES;
+      const int gg = min(g, G - 1) - (j >> 3) * 8 * NSEG;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) x[rt] = *reinterpret_cast<const float*>(xc + x_slot<XP>(xr[rt], gg));
+    }
+    v4f t[NT];
+    skinny_group<RT, CT, DOTS>(P, c0, lane, live && g < G, g, aq[d], bq[d], x, wq[d], t);
+    if constexpr (!DOTS) {
+#pragma unroll
+      for (int k = 0; k < NT; ++k) tb[j & 1][wid][k][lane] = t[k];
+    }
+  };
+  int j0 = 0;
+  for (; j0 + DB <= steps; j0 += DB) {
+#pragma unroll
+    for (int d = 0; d < DB; ++d) step(j0 + d, d);
+  }
+#pragma unroll
+  for (int d = 0; d < DB - 1; ++d)
+    if (j0 + d < steps) step(j0 + d, d);
+  if constexpr (!DOTS) {
+    lds_barrier();
+    add_posted(steps - 1);
+  }
+  wait_vmcnt<0>();  // the clamped loads past the end
+  if constexpr (!DOTS)
+    if (live && sidx == 0) skinny_store<RT, CT>(P, c0, lane, s);
+}
+
+template <int RT, int CT, int CTL, int DBS, int DBL, bool DOTS>
+__global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[skinny_lds_bytes(RT, CTL)];
+  const int lane = threadIdx.x & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const Proj& P = b.p[find_proj(b, blockIdx.x)];
+  const int local = blockIdx.x - P.wave_begin;
+  if (P.nseg == 1)
+    skinny_short<RT, CT, DBS, DOTS>(P, local, wid, lane, lds);
+  else
+    skinny_long<RT, CTL, DBL, 4, DOTS>(P, local, wid, lane, lds);
+}
 }  // namespace
 
 static unsigned blocks_for(long n, int per) { return (unsigned)((n + per - 1) / per); }
@@ -751,17 +980,24 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
   return hipGetLastError();
 }
 
-#ifndef DQ8_SKINNY_DEPTH
-#define DQ8_SKINNY_DEPTH 4
+// Skinny launch shape (tunable at build time): a short-K wave covers 16*CT
+// columns, a long-K wave 16*CTL; DBS / DBL steps in flight in their rings.
+#ifndef DQ8_SKINNY_CT
+#define DQ8_SKINNY_CT 2
 #endif
-int skinny_cols() { return 16; }
-// Waves per skinny tile: projections with more than DQ8_SKINNY_SPLIT groups
-// interleave each tile's groups over 2 (up to twice that) or 4 waves.
-#ifndef DQ8_SKINNY_SPLIT
-#define DQ8_SKINNY_SPLIT 32
+#ifndef DQ8_SKINNY_CTL
+#define DQ8_SKINNY_CTL 1
 #endif
-int skinny_row_waves(int m) { return (m + 15) / 16; }
-int skinny_segments(int g) { return g <= DQ8_SKINNY_SPLIT ? 1 : g <= 2 * DQ8_SKINNY_SPLIT ? 2 : 4; }
+#ifndef DQ8_SKINNY_DBS
+#define DQ8_SKINNY_DBS 4
+#endif
+#ifndef DQ8_SKINNY_DBL
+#define DQ8_SKINNY_DBL 6
+#endif
+// Short K (G <= 32) runs one wave per strip; longer K interleaves a strip's
+// groups over 4 waves.
+int skinny_segments(int g) { return g <= 32 ? 1 : 4; }
+int skinny_cols(int g) { return 16 * (skinny_segments(g) == 1 ? DQ8_SKINNY_CT : DQ8_SKINNY_CTL); }
 int wide_block_rows() { return 32 * DQ8_WIDE_RT * DQ8_WIDE_WM; }
 int wide_block_cols() { return 32 * DQ8_WIDE_CT * DQ8_WIDE_WN; }
 
@@ -778,9 +1014,15 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
           <<<b.total_waves, threads, 0, s>>>(b);
     return hipGetLastError();
   }
-  // total_waves counts blocks of 4 waves for the skinny kernel
-  if (dots) k_linear_skinny<DQ8_SKINNY_DEPTH, true><<<b.total_waves, 256, 0, s>>>(b);
-  else k_linear_skinny<DQ8_SKINNY_DEPTH, false><<<b.total_waves, 256, 0, s>>>(b);
+  // total_waves counts blocks of 4 waves for the skinny kernel; kind 1: M <= 16, kind 2: M <= 32
+  constexpr int CT = DQ8_SKINNY_CT, CL = DQ8_SKINNY_CTL, DS = DQ8_SKINNY_DBS, DL = DQ8_SKINNY_DBL;
+  if (kind == 1) {
+    if (dots) k_linear_skinny<1, CT, CL, DS, DL, true><<<b.total_waves, 256, 0, s>>>(b);
+    else k_linear_skinny<1, CT, CL, DS, DL, false><<<b.total_waves, 256, 0, s>>>(b);
+  } else {
+    if (dots) k_linear_skinny<2, CT, CL, DS, DL, true><<<b.total_waves, 256, 0, s>>>(b);
+    else k_linear_skinny<2, CT, CL, DS, DL, false><<<b.total_waves, 256, 0, s>>>(b);
+  }
   return hipGetLastError();
 }
 

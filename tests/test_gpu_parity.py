@@ -118,7 +118,8 @@ def test_weights_from_quantized_round_trip(ctx, n, k):
 
 # -------------------------------------------------------------- group dots
 
-DOT_SHAPES = [(1, 64, 1), (5, 100, 9), (24, 2048, 33), (32, 131, 70), (33, 64, 31), (67, 192, 65), (130, 257, 40)]
+DOT_SHAPES = [(1, 64, 1), (5, 100, 9), (24, 2048, 33), (32, 131, 70), (33, 64, 31), (67, 192, 65), (130, 257, 40),
+              (24, 6144, 20), (17, 2371, 33), (9, 4160, 18)]
 
 
 @pytest.mark.parametrize("m,k,n", DOT_SHAPES)
@@ -144,8 +145,12 @@ def test_group_dots_extremes(ctx):
 
 # ---------------------------------------------------------------- projection
 
+# Skinny (M <= 32) cases cover both row-tile counts (M <= 16, M <= 32), short K
+# (G <= 32, odd G, G = 1) and long K (G > 32: 4-way split groups, partial last
+# step, several x-scale chunks, K % 64 != 0).
 LINEAR_SHAPES = [(1, 1, 1), (1, 64, 4), (4, 64, 4), (5, 128, 6), (9, 192, 31), (24, 2048, 100), (32, 131, 70),
-                 (33, 100, 9), (67, 128, 8), (64, 2048, 64), (128, 2048, 130), (200, 65, 17), (7, 6144, 33)]
+                 (33, 100, 9), (67, 128, 8), (64, 2048, 64), (128, 2048, 130), (200, 65, 17), (7, 6144, 33),
+                 (24, 6144, 70), (17, 2371, 50), (32, 4096, 40), (16, 2112, 33), (2, 2113, 17)]
 
 
 @pytest.mark.parametrize("m,k,n", LINEAR_SHAPES)
@@ -253,6 +258,34 @@ def test_linear_batch_mixed_kinds_matches_single_calls(ctx):
     ctx.linear_batch(items)
     for it, want in zip(items, wants):
         assert bits_equal(host(it.out), want)
+
+
+def test_linear_batch_question_layer_set(ctx):
+    # One continuation question (M=24) against a scaled-down layer set: short-K
+    # and long-K skinny projections in one grouped launch, with bias and epilogues.
+    rng = np.random.default_rng(24)
+    m = 24
+    items, wants = [], []
+    for (k, n, ep) in [(256, 96, dq8.WRITE), (256, 40, dq8.WRITE), (256, 200, dq8.WRITE), (2048, 64, dq8.WRITE),
+                       (2048, 96, dq8.SWIGLU), (6144, 64, dq8.ADD), (2240, 33, dq8.WRITE)]:
+        x = make_x(rng, m, k)
+        w = make_w(rng, n, k)
+        bias = rng.standard_normal(n).astype(np.float32)
+        wv, ws = dq8o.quantize_weights(w)
+        h = ctx.weights_from_quantized(dev(wv), dev(ws))
+        q, s = ctx.quantize(dev(x))
+        base = rng.standard_normal((m, n)).astype(np.float32)
+        out = dev(base.copy())
+        items.append(dq8.Item(h, q, s, out, bias=dev(bias), epilogue=ep))
+        wants.append((dq8o.linear(x, wv, ws, bias=bias, result=base, epilogue=ep, threads=4), ep != dq8.SWIGLU))
+    ctx.linear_batch(items)
+    for it, (want, exact) in zip(items, wants):
+        got = host(it.out)
+        if exact:
+            assert bits_equal(got, want)
+        else:
+            rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
+            assert float(rel.max()) <= SWIGLU_RTOL
 
 
 def test_config1_single_linear_seed0_bit_exact(ctx):
