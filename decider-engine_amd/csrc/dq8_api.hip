@@ -89,7 +89,12 @@ dq8_status make_weights(dq8_ctx* ctx, size_t n, size_t k, dq8_weights** out) {
 
 // Fill a launch item.  q must already satisfy the kernel's requirements.
 void fill_proj(dq8::Proj& p, const dq8::Weights& w, const int8_t* q, int ldq, const float* xs, int ldxs, size_t m,
-               const float* bias, float* out, int32_t* dots, int layout, int epilogue) {
+               const float* bias, float* out, int32_t* dots, int layout, int epilogue, const dq8_lora* lora) {
+  p.lmid = lora ? lora->mid : nullptr;
+  p.lb = lora ? lora->b : nullptr;
+  p.lora = lora != nullptr;
+  p.rank = lora ? (int)lora->rank : 0;
+  p.lscale = lora ? lora->scale : 0.0f;
   p.q = q;
   p.xs = xs;
   p.ldxs = ldxs;
@@ -163,6 +168,16 @@ size_t xs_pad_bytes(const dq8::Weights& w, size_t m) {
   return (m * (size_t)padded_groups(w) * sizeof(float) + 255) / 256 * 256;
 }
 
+// A LoRA pair needs its two matrices unless its rank is 0 (then only the
+// crate's `+ scale * (0.0 + 0.0)` remains); mid [m][rank] and b [n][rank] are
+// read at rank floats per row.
+dq8_status check_lora(const dq8_lora* lora) {
+  if (!lora) return DQ8_OK;
+  if (lora->rank > (1u << 20)) return DQ8_ERR_SHAPE;
+  if (lora->rank > 0 && (!lora->mid || !lora->b)) return DQ8_ERR_ARG;
+  return DQ8_OK;
+}
+
 dq8_status check_item_args(const dq8_weights* w, const int8_t* q, const float* scales, size_t m, float* out,
                            dq8_layout layout, dq8_epilogue epilogue) {
   if (!w || !q || !scales || !out) return DQ8_ERR_ARG;
@@ -187,7 +202,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     if (st != DQ8_OK) return st;
   }
   dq8::Batch batch[dq8::kKinds];
-  for (dq8::Batch& b : batch) b.count = b.total_waves = 0;
+  for (dq8::Batch& b : batch) b.count = b.total_waves = b.any_lora = 0;
   size_t offset = 0;
   // Two passes: projections with long K (more than 32 groups) first, so their
   // blocks start when the launch does instead of trailing the short ones.
@@ -204,6 +219,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
       if (e != hipSuccess) return from_hip(e);
       b.count = 0;
       b.total_waves = 0;
+      b.any_lora = 0;
     }
     const int8_t* q = it.q;
     int ldq = w.k;
@@ -226,7 +242,8 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
       offset += xs_pad_bytes(w, it.m);
     }
     dq8::Proj& p = b.p[b.count++];
-    fill_proj(p, w, q, ldq, xs, ldxs, it.m, it.bias, it.out, dots, it.layout, it.epilogue);
+    fill_proj(p, w, q, ldq, xs, ldxs, it.m, it.bias, it.out, dots, it.layout, it.epilogue, dots ? nullptr : it.lora);
+    if (p.lora) b.any_lora = 1;
     place_proj(p, kind, b);
   }
   for (int kind = 0; kind < dq8::kKinds; ++kind) {
@@ -376,8 +393,34 @@ dq8_status dq8_linear(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, const
   if (st != DQ8_OK) return st;
   if (w->w.device != ctx->device) return DQ8_ERR_ARG;
   DeviceGuard guard(ctx->device);
-  dq8_linear_item it = {w, q, scales, m, bias, out, layout, epilogue};
+  dq8_linear_item it = {w, q, scales, m, bias, out, layout, epilogue, nullptr};
   return run_linear(ctx, &it, 1, nullptr, (hipStream_t)stream);
+}
+
+dq8_status dq8_linear_lora(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, const float* scales, size_t m,
+                           const float* bias, const dq8_lora* lora, float* out, dq8_layout layout,
+                           dq8_epilogue epilogue, void* stream) {
+  if (!ctx) return DQ8_ERR_ARG;
+  if (m == 0) return w ? DQ8_OK : DQ8_ERR_ARG;
+  dq8_status st = check_item_args(w, q, scales, m, out, layout, epilogue);
+  if (st == DQ8_OK) st = check_lora(lora);
+  if (st != DQ8_OK) return st;
+  if (w->w.device != ctx->device) return DQ8_ERR_ARG;
+  DeviceGuard guard(ctx->device);
+  dq8_linear_item it = {w, q, scales, m, bias, out, layout, epilogue, lora};
+  return run_linear(ctx, &it, 1, nullptr, (hipStream_t)stream);
+}
+
+dq8_status dq8_lora_mid(dq8_ctx* ctx, const float* x, size_t m, size_t k, const float* a, size_t rank, float* mid,
+                        void* stream) {
+  if (!ctx) return DQ8_ERR_ARG;
+  if (m == 0 || rank == 0) return DQ8_OK;
+  if (!x || !a || !mid) return DQ8_ERR_ARG;
+  if (k == 0 || m > (1u << 30) || k > (1u << 30) || rank > (1u << 20) || m * k > ((size_t)1 << 40) ||
+      rank * k > ((size_t)1 << 40))
+    return DQ8_ERR_SHAPE;
+  DeviceGuard guard(ctx->device);
+  return from_hip(dq8::launch_lora_mid(x, (int)m, (int)k, a, (int)rank, mid, (hipStream_t)stream));
 }
 
 dq8_status dq8_linear_batch(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, void* stream) {
@@ -389,6 +432,7 @@ dq8_status dq8_linear_batch(dq8_ctx* ctx, const dq8_linear_item* items, size_t c
     }
     dq8_status st = check_item_args(items[i].w, items[i].q, items[i].scales, items[i].m, items[i].out,
                                     items[i].layout, items[i].epilogue);
+    if (st == DQ8_OK) st = check_lora(items[i].lora);
     if (st != DQ8_OK) return st;
     if (items[i].w->w.device != ctx->device) return DQ8_ERR_ARG;
   }
@@ -424,8 +468,9 @@ dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, 
   dq8::Batch b;
   b.count = 1;
   dq8::Proj& p = b.p[0];
-  fill_proj(p, w->w, q, (int)ldq, xs, ldxs, m, bias, out, nullptr, layout, epilogue);
+  fill_proj(p, w->w, q, (int)ldq, xs, ldxs, m, bias, out, nullptr, layout, epilogue, nullptr);
   b.total_waves = 0;
+  b.any_lora = 0;
   const int kind = kind_of(w->w, m);
   place_proj(p, kind, b);
   return from_hip(dq8::launch_linear(b, kind, false, s));
@@ -437,7 +482,7 @@ dq8_status dq8_group_dots(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, s
   if (m == 0) return DQ8_OK;
   DeviceGuard guard(ctx->device);
   // Scales are not read by the dots kernels; pass the weights' own as a valid pointer.
-  dq8_linear_item it = {w, q, w->w.scales, m, nullptr, nullptr, DQ8_ROWS, DQ8_WRITE};
+  dq8_linear_item it = {w, q, w->w.scales, m, nullptr, nullptr, DQ8_ROWS, DQ8_WRITE, nullptr};
   return run_linear(ctx, &it, 1, dots, (hipStream_t)stream);
 }
 

@@ -34,6 +34,11 @@ struct Proj {
   const float* bias;  // [N] or null
   float* out;
   int32_t* dots;      // debug output [M][N][G] (dots kernels only)
+  const float* lmid;  // LoRA middle product [M][rank] (read only when rank > 0)
+  const float* lb;    // LoRA B [N][rank]
+  int lora;           // the projection has an adapter
+  int rank;
+  float lscale;
   int m, ldq, ldxs, g, n, np;
   int epilogue;       // 0 write, 1 add, 2 swiglu
   int layout;         // 0 rows [M][N], 1 columns [N][M]
@@ -47,6 +52,7 @@ struct Batch {
   Proj p[kMaxBatch];
   int count;
   int total_waves;  // blocks of the launch
+  int any_lora;     // some projection has a LoRA adapter (selects the kernels with the LoRA epilogue)
 };
 
 // Kernel launchers (dq8_kernels.hip).  All return hipError_t of the launch.
@@ -57,6 +63,8 @@ hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int 
 hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipStream_t s);
 hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ldq, hipStream_t s);
 hipError_t launch_pad_scales(const float* xs, int rows, int g, float* dst, int ld, hipStream_t s);
+// LoRA middle product mid [m][rank] = dot_scores(x_r, a_j) + 0.0 (x [m][k], a [rank][k]).
+hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int rank, float* mid, hipStream_t s);
 // Kind: 0 wide (M > 32), 1 skinny (M <= 16), 2 skinny (16 < M <= 32).  dots
 // selects the debug kernel.
 constexpr int kKinds = 3;

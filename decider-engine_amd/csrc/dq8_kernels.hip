@@ -92,6 +92,30 @@ __device__ __forceinline__ int find_proj(const Batch& b, int wave) {
   return pi;
 }
 
+// LoRA term of Adapter::combine (tensor.rs:109-117) for one MFMA tile set:
+// out = base + scale * (dot_scores(mid[row], b[col]) + 0.0), dot_scores in its
+// x86-64 order (tensor.rs:6-25): lane i of 8 sums the products of elements i,
+// i+8, ...; the lanes are added in order, then the tail elements one by one.
+// prod(i) returns the tile's products mid[row][i] * b[col][i] (each one rounded
+// product, from a K=1 MFMA with C = 0).  The reference starts its lanes at 0.0
+// and their sum at -0.0; starting from the first product instead only changes
+// the sign of an all-zero partial sum, and the final + 0.0 makes every zero
+// delta +0.0 in both, so the result is identical.
+template <typename V, typename Prod>
+__device__ __forceinline__ V lora_term(const V& base, const V& zero, int rank, float scale, Prod prod) {
+  const int chunks = rank >> 3;
+  V sum = zero;  // no full chunk: eight +0.0 lanes sum to +0.0
+  if (chunks > 0) {
+    for (int i = 0; i < 8; ++i) {
+      V ln = prod(i);
+      for (int c = 1; c < chunks; ++c) ln = ln + prod(8 * c + i);
+      sum = i == 0 ? ln : sum + ln;
+    }
+  }
+  for (int t = 8 * chunks; t < rank; ++t) sum = sum + prod(t);
+  return base + scale * (sum + zero);
+}
+
 // ---------------------------------------------------------------------------
 // Quantization: QuantizedInputs::new (tensor.rs:321-339) and the 8-bit
 // Data::quantize (weights.rs:117-136).  One wave covers 256 consecutive
@@ -342,7 +366,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 #else
 #define DQ8_WIDE_ATTR
 #endif
-template <int WM, int WN, int RT, int CT, int STAGES, int XCH, int SWZ, bool DOTS>
+template <int WM, int WN, int RT, int CT, int STAGES, int XCH, int SWZ, bool DOTS, bool LORA>
 __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batch b) {
   constexpr int NW = WM * WN, WR = 32 * RT, WC = 32 * CT;
   constexpr int BM = WR * WM, BN = WC * WN;
@@ -542,6 +566,20 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       const int col = nw + 32 * c + (lane & 31);
       bias[c] = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
     }
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+      for (int v = 0; v < 32; ++v) s[j][v] = s[j][v] + bias[RT == 2 ? j : v >> 4];
+    if (LORA && P.lora) {
+      // then + scale * (mid . b + 0.0) (tensor.rs:438, 109-117); the K=1 MFMA
+      // operands follow the x/w scale convention of the group loop.
+      const float* lm = P.lmid + (size_t)min(mw + (RT == 2 ? lane : (lane & 31)), P.m - 1) * P.rank;
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        const float* lbc = P.lb + (size_t)min(nw + (RT == 2 ? 32 * j + (lane & 31) : lane), P.n - 1) * P.rank;
+        s[j] = lora_term(s[j], zero32, P.rank, P.lscale, [&](int i) { return mfma_k1(lm[i], lbc[i], zero32); });
+      }
+    }
     constexpr int E = NP * 32;
     int rows[E], cols[E];
     float y[E];
@@ -553,7 +591,7 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
         const int r = RT == 2 ? blk2 : 0, c = RT == 2 ? j : blk2;
         rows[32 * j + v] = mw + 32 * r + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);
         cols[32 * j + v] = nw + 32 * c + (lane & 31);
-        y[32 * j + v] = s[j][v] + bias[c];
+        y[32 * j + v] = s[j][v];
       }
     store_tile(P, rows, cols, y);
   }
@@ -632,26 +670,46 @@ __device__ __forceinline__ void issue_x_chunk(const Proj& P, int c, int wid, uin
   }
 }
 
-// y = s + bias, or s + 0.0f without a bias (tensor.rs:437), stored by the epilogue.
-template <int RT, int CT>
-__device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, const v4f (&s)[RT * CT]) {
+// y = s + bias, or s + 0.0f without a bias (tensor.rs:437), then the LoRA term
+// (tensor.rs:438, 109-117) when the projection has an adapter, stored by the
+// epilogue.  LoRA products: K=1 MFMA with A lane a = mid of row 4*(a/16) + a%4
+// and B lane l = b of column l%16, the x/w scale convention of the group loop.
+template <int RT, int CT, bool LORA>
+__device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, v4f (&s)[RT * CT]) {
   constexpr int E = 4 * RT * CT;
-  int rows[E], cols[E];
-  float y[E];
+  const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const int col = c0 + 16 * ct + (lane & 15);
     const float bias = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) s[rt * CT + ct] = s[rt * CT + ct] + bias;
+  }
+  if (LORA && P.lora) {
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const float* lm = P.lmid + (size_t)min(16 * rt + 4 * (lane >> 4) + (lane & 3), P.m - 1) * P.rank;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const float* lbc = P.lb + (size_t)min(c0 + 16 * ct + (lane & 15), P.n - 1) * P.rank;
+        s[rt * CT + ct] = lora_term(s[rt * CT + ct], zero4, P.rank, P.lscale,
+                                    [&](int i) { return mfma_k1_4(lm[i], lbc[i], zero4); });
+      }
+    }
+  }
+  int rows[E], cols[E];
+  float y[E];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int e = 4 * (rt * CT + ct) + v;
         rows[e] = 16 * rt + 4 * (lane >> 4) + v;
-        cols[e] = col;
-        y[e] = s[rt * CT + ct][v] + bias;
+        cols[e] = c0 + 16 * ct + (lane & 15);
+        y[e] = s[rt * CT + ct][v];
       }
-  }
   store_tile(P, rows, cols, y);
 }
 
@@ -685,7 +743,7 @@ __device__ __forceinline__ void skinny_group(const Proj& P, int c0, int lane, bo
 }
 
 // Short K (G <= 32): 4 strips per block, one wave each, 2 groups per step.
-template <int RT, int CT, int DB, bool DOTS>
+template <int RT, int CT, int DB, bool DOTS, bool LORA>
 __device__ __forceinline__ void skinny_short(const Proj& P, int local, int wid, int lane, uint8_t* lds) {
   constexpr int ROWS = 16 * RT;
   constexpr int STEP_A = RT * 2 * kFragBytes;  // activation bytes of one step (8-row units)
@@ -795,11 +853,11 @@ __device__ __forceinline__ void skinny_short(const Proj& P, int local, int wid, 
     if (j0 + d < steps) step(j0 + d, d);
   wait_vmcnt<0>();  // the clamped loads past the end
   if constexpr (!DOTS)
-    if (live) skinny_store<RT, CT>(P, c0, lane, s);
+    if (live) skinny_store<RT, CT, LORA>(P, c0, lane, s);
 }
 
 // Long K (G > 32): 4/NSEG strips per block, NSEG waves each, one group per wave and step.
-template <int RT, int CT, int DB, int NSEG, bool DOTS>
+template <int RT, int CT, int DB, int NSEG, bool DOTS, bool LORA>
 __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, int lane, uint8_t* lds) {
   constexpr int ROWS = 16 * RT, NT = RT * CT, TPB = 4 / NSEG;
   constexpr int XP = 2 * NSEG;                 // x pieces per row of a chunk of 8 steps (8*NSEG groups)
@@ -924,10 +982,10 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
   }
   wait_vmcnt<0>();  // the clamped loads past the end
   if constexpr (!DOTS)
-    if (live && sidx == 0) skinny_store<RT, CT>(P, c0, lane, s);
+    if (live && sidx == 0) skinny_store<RT, CT, LORA>(P, c0, lane, s);
 }
 
-template <int RT, int CT, int CTL, int DBS, int DBL, bool DOTS>
+template <int RT, int CT, int CTL, int DBS, int DBL, bool DOTS, bool LORA>
 __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[skinny_lds_bytes(RT, CTL)];
   const int lane = threadIdx.x & 63;
@@ -935,13 +993,65 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   const Proj& P = b.p[find_proj(b, blockIdx.x)];
   const int local = blockIdx.x - P.wave_begin;
   if (P.nseg == 1)
-    skinny_short<RT, CT, DBS, DOTS>(P, local, wid, lane, lds);
+    skinny_short<RT, CT, DBS, DOTS, LORA>(P, local, wid, lane, lds);
   else
-    skinny_long<RT, CTL, DBL, 4, DOTS>(P, local, wid, lane, lds);
+    skinny_long<RT, CTL, DBL, 4, DOTS, LORA>(P, local, wid, lane, lds);
 }
+// LoRA middle product (weights.rs:480, 495): mid[r][j] = dot_scores(x_r, a_j)
+// + 0.0 for x [m][k], a [rank][k], in dot_scores' x86-64 order (tensor.rs:6-25).
+// A wave covers 4 rows and 8 columns j: lane l works on column j0 + l/8 and
+// holds lane i = l%8 of its partial sums (elements i, i+8, ...) for the 4 rows.
+// The 8 partial sums are then added in order, the tail elements one by one.
+__global__ __launch_bounds__(256) void k_lora_mid(const float* __restrict__ x, int m, int k, const float* __restrict__ a,
+                                                  int rank, float* __restrict__ mid) {
+  const int lane = threadIdx.x & 63;
+  const long wave = (long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int jblocks = (rank + 7) >> 3;
+  if (wave >= (long)((m + 3) >> 2) * jblocks) return;  // wave-uniform
+  const int r0 = (int)(wave / jblocks) * 4;
+  const int j = (int)(wave % jblocks) * 8 + (lane >> 3), i = lane & 7;
+  const float* arow = a + (size_t)min(j, rank - 1) * k;
+  const float* xr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) xr[r] = x + (size_t)min(r0 + r, m - 1) * k;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int chunks = k >> 3;
+  for (int c = 0; c < chunks; ++c) {
+    const float av = arow[8 * c + i];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = acc[r] + xr[r][8 * c + i] * av;
+  }
+  float sum[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float t = -0.0f;
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii) t = t + __shfl(acc[r], (lane & ~7) + ii);
+    sum[r] = t;
+  }
+  for (int t = 8 * chunks; t < k; ++t) {
+    const float av = arow[t];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sum[r] = sum[r] + xr[r][t] * av;
+  }
+  if (i == 0 && j < rank) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (r0 + r < m) mid[(size_t)(r0 + r) * rank + j] = sum[r] + 0.0f;
+  }
+}
+
 }  // namespace
 
 static unsigned blocks_for(long n, int per) { return (unsigned)((n + per - 1) / per); }
+
+hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int rank, float* mid, hipStream_t s) {
+  const long waves = (long)((m + 3) / 4) * ((rank + 7) / 8);
+  if (waves == 0) return hipSuccess;
+  k_lora_mid<<<blocks_for(waves, 4), 256, 0, s>>>(x, m, k, a, rank, mid);
+  return hipGetLastError();
+}
+
 
 hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
                            uint32_t* nonfinite, hipStream_t s) {
@@ -1003,26 +1113,32 @@ int wide_block_cols() { return 32 * DQ8_WIDE_CT * DQ8_WIDE_WN; }
 
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
   if (b.total_waves == 0) return hipSuccess;
+  const bool lora = !dots && b.any_lora;
   if (kind == 0) {
     // total_waves counts blocks for the wide kernel
     constexpr int threads = 64 * DQ8_WIDE_WM * DQ8_WIDE_WN;
-    if (dots)
-      k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_XCH, DQ8_WIDE_SWZ, true>
-          <<<b.total_waves, threads, 0, s>>>(b);
-    else
-      k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_XCH, DQ8_WIDE_SWZ, false>
-          <<<b.total_waves, threads, 0, s>>>(b);
+#define DQ8_WIDE(D, L)                                                                                     \
+  k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_XCH, DQ8_WIDE_SWZ, \
+                D, L><<<b.total_waves, threads, 0, s>>>(b)
+    if (dots) DQ8_WIDE(true, false);
+    else if (lora) DQ8_WIDE(false, true);
+    else DQ8_WIDE(false, false);
+#undef DQ8_WIDE
     return hipGetLastError();
   }
   // total_waves counts blocks of 4 waves for the skinny kernel; kind 1: M <= 16, kind 2: M <= 32
   constexpr int CT = DQ8_SKINNY_CT, CL = DQ8_SKINNY_CTL, DS = DQ8_SKINNY_DBS, DL = DQ8_SKINNY_DBL;
+#define DQ8_SKINNY(R, D, L) k_linear_skinny<R, CT, CL, DS, DL, D, L><<<b.total_waves, 256, 0, s>>>(b)
   if (kind == 1) {
-    if (dots) k_linear_skinny<1, CT, CL, DS, DL, true><<<b.total_waves, 256, 0, s>>>(b);
-    else k_linear_skinny<1, CT, CL, DS, DL, false><<<b.total_waves, 256, 0, s>>>(b);
+    if (dots) DQ8_SKINNY(1, true, false);
+    else if (lora) DQ8_SKINNY(1, false, true);
+    else DQ8_SKINNY(1, false, false);
   } else {
-    if (dots) k_linear_skinny<2, CT, CL, DS, DL, true><<<b.total_waves, 256, 0, s>>>(b);
-    else k_linear_skinny<2, CT, CL, DS, DL, false><<<b.total_waves, 256, 0, s>>>(b);
+    if (dots) DQ8_SKINNY(2, true, false);
+    else if (lora) DQ8_SKINNY(2, false, true);
+    else DQ8_SKINNY(2, false, false);
   }
+#undef DQ8_SKINNY
   return hipGetLastError();
 }
 

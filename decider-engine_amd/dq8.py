@@ -39,6 +39,15 @@ class NonFinite(Dq8Error):
     """The reference's `None` from QuantizedInputs::new: the input holds NaN or +-inf."""
 
 
+class _Lora(ctypes.Structure):
+    _fields_ = [
+        ("mid", ctypes.c_void_p),
+        ("b", ctypes.c_void_p),
+        ("rank", ctypes.c_size_t),
+        ("scale", ctypes.c_float),
+    ]
+
+
 class _Item(ctypes.Structure):
     _fields_ = [
         ("w", ctypes.c_void_p),
@@ -49,6 +58,7 @@ class _Item(ctypes.Structure):
         ("out", ctypes.c_void_p),
         ("layout", ctypes.c_int),
         ("epilogue", ctypes.c_int),
+        ("lora", ctypes.POINTER(_Lora)),
     ]
 
 
@@ -82,6 +92,8 @@ def lib() -> ctypes.CDLL:
         "dq8_linear": ([_vp, _vp, _vp, _vp, _sz, _vp, _vp, _i, _i, _vp], _i),
         "dq8_linear_f32in": ([_vp, _vp, _vp, _sz, _vp, _vp, _i, _i, _vp], _i),
         "dq8_linear_batch": ([_vp, ctypes.POINTER(_Item), _sz, _vp], _i),
+        "dq8_lora_mid": ([_vp, _vp, _sz, _sz, _vp, _sz, _vp, _vp], _i),
+        "dq8_linear_lora": ([_vp, _vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
         "dq8_group_dots": ([_vp, _vp, _vp, _sz, _vp, _vp], _i),
         "dq8_status_string": ([_i], ctypes.c_char_p),
     }
@@ -159,6 +171,16 @@ class Weights:
 
 
 @dataclass
+class Lora:
+    """A projection's LoRA pair as the reference's Adapter holds it (tensor.rs:102-108):
+    mid [m][rank] (Context.lora_mid of x and lora_A), b = lora_B [n][rank], scale."""
+
+    mid: object
+    b: object
+    scale: float
+
+
+@dataclass
 class Item:
     """One projection of Context.linear_batch."""
 
@@ -169,6 +191,7 @@ class Item:
     bias: object = None
     layout: int = ROWS
     epilogue: int = WRITE
+    lora: Lora | None = None
 
 
 class Context:
@@ -257,6 +280,49 @@ class Context:
                                 out.data_ptr(), layout, epilogue, _stream(self.device)), "dq8_linear")
         return out
 
+    # -- LoRA ----------------------------------------------------------
+    def lora_mid(self, x, a, mid=None):
+        """mid [m][rank] = linear(x, lora_A) in the reference's FP32 order (weights.rs:480, 495)."""
+        torch = _torch()
+        self._dev(x, torch.float32, name="x")
+        self._dev(a, torch.float32, name="lora_A")
+        m, k = x.shape
+        rank, ka = a.shape
+        if ka != k:
+            raise Dq8Error(ERR_SHAPE, "dq8_lora_mid: lora_A width differs from the input")
+        if mid is None:
+            mid = torch.zeros((m, rank), dtype=torch.float32, device=self.device)
+        self._dev(mid, torch.float32, (m, rank), "mid")
+        _check(lib().dq8_lora_mid(self.handle, x.data_ptr(), m, k, a.data_ptr(), rank, mid.data_ptr(),
+                                  _stream(self.device)), "dq8_lora_mid")
+        return mid
+
+    def _lora(self, lora: Lora, m: int, n: int) -> _Lora:
+        torch = _torch()
+        rank = lora.b.shape[1]
+        self._dev(lora.mid, torch.float32, (m, rank), "lora mid")
+        self._dev(lora.b, torch.float32, (n, rank), "lora_B")
+        return _Lora(lora.mid.data_ptr(), lora.b.data_ptr(), rank, lora.scale)
+
+    def linear_lora(self, w: Weights, q, scales, lora: Lora, out=None, bias=None, layout=ROWS, epilogue=WRITE):
+        torch = _torch()
+        self._dev(q, torch.int8, name="q")
+        m, k = q.shape
+        if k != w.k:
+            raise Dq8Error(ERR_SHAPE, "dq8_linear_lora: input width differs from the weights")
+        self._dev(scales, torch.float32, (m, groups(k)), "scales")
+        shape = (m, w.n) if layout == ROWS else (w.n, m)
+        if out is None:
+            out = torch.zeros(shape, dtype=torch.float32, device=self.device)
+        self._dev(out, torch.float32, shape, "out")
+        if bias is not None:
+            self._dev(bias, torch.float32, (w.n,), "bias")
+        lo = self._lora(lora, m, w.n)
+        _check(lib().dq8_linear_lora(self.handle, w.handle, q.data_ptr(), scales.data_ptr(), m, _ptr(bias),
+                                     ctypes.byref(lo), out.data_ptr(), layout, epilogue, _stream(self.device)),
+               "dq8_linear_lora")
+        return out
+
     def linear_f32in(self, w: Weights, x, out=None, bias=None, layout=ROWS, epilogue=WRITE):
         torch = _torch()
         self._dev(x, torch.float32, name="x")
@@ -276,6 +342,7 @@ class Context:
     def linear_batch(self, items: list[Item]) -> None:
         torch = _torch()
         arr = (_Item * max(1, len(items)))()
+        keep = []  # the _Lora structs must outlive the call
         for i, it in enumerate(items):
             self._dev(it.q, torch.int8, name="q")
             m, k = it.q.shape
@@ -284,8 +351,12 @@ class Context:
             self._dev(it.scales, torch.float32, (m, groups(k)), "scales")
             shape = (m, it.w.n) if it.layout == ROWS else (it.w.n, m)
             self._dev(it.out, torch.float32, shape, "out")
+            lp = None
+            if it.lora is not None:
+                keep.append(self._lora(it.lora, m, it.w.n))
+                lp = ctypes.pointer(keep[-1])
             arr[i] = _Item(it.w.handle, it.q.data_ptr(), it.scales.data_ptr(), m, _ptr(it.bias), it.out.data_ptr(),
-                           it.layout, it.epilogue)
+                           it.layout, it.epilogue, lp)
         _check(lib().dq8_linear_batch(self.handle, arr, len(items), _stream(self.device)), "dq8_linear_batch")
 
     def group_dots(self, w: Weights, q):

@@ -104,8 +104,36 @@ dq8_status dq8_linear(dq8_ctx *ctx, const dq8_weights *w, const int8_t *q, const
 dq8_status dq8_linear_f32in(dq8_ctx *ctx, const dq8_weights *w, const float *x, size_t m, const float *bias,
                             float *out, dq8_layout layout, dq8_epilogue epilogue, void *stream);
 
+/* The LoRA pair of a projection as Adapter (tensor.rs:102-108) holds it:
+ *   mid   fp32 [m][rank]  the middle product x . A^T (dq8_lora_mid)
+ *   b     fp32 [n][rank]  lora_B (weights.rs:427), the crate's FP32 Data::F32
+ *   scale                 the adapter scale
+ * Every output becomes y = (s + bias) + scale * (dot_scores(mid[row], b[col]) + 0.0)
+ * (Adapter::combine, tensor.rs:109-117), with dot_scores in its x86-64 order
+ * (tensor.rs:6-25) and every product and sum rounded on its own.  That is what
+ * both of the crate's schedules produce: the per-output combine (m < 64) and the
+ * separate B pass of Projection::apply_quantized (m >= 64, tensor.rs:155-179), and
+ * the x86 plan of Linear::apply_into_shared (weights.rs:450-491).  The struct is
+ * host memory; mid and b are device pointers. */
+typedef struct dq8_lora {
+    const float *mid;
+    const float *b;
+    size_t rank;
+    float scale;
+} dq8_lora;
+/* LoRA middle product (Linear::apply_into_shared, weights.rs:480 and 495):
+ * mid [m][rank] = linear(x, A) with x fp32 [m][k] and A = lora_A fp32 [rank][k],
+ * i.e. mid[r][j] = dot_scores(x_r, A_j) + 0.0 (the FP32 columns of
+ * tensor.rs:206-269 without bias).  Non-finite inputs propagate as in the crate. */
+dq8_status dq8_lora_mid(dq8_ctx *ctx, const float *x, size_t m, size_t k, const float *a, size_t rank, float *mid,
+                        void *stream);
+/* dq8_linear with the projection's LoRA adapter (Projection::apply_quantized with
+ * `adapter`, tensor.rs:134-183).  lora == NULL is dq8_linear. */
+dq8_status dq8_linear_lora(dq8_ctx *ctx, const dq8_weights *w, const int8_t *q, const float *scales, size_t m,
+                           const float *bias, const dq8_lora *lora, float *out, dq8_layout layout,
+                           dq8_epilogue epilogue, void *stream);
 /* Several independent projections in one launch (same-shape inputs are not
- * required).  Each item is one dq8_linear.  This is the shape of a model
+ * required).  Each item is one dq8_linear (or dq8_linear_lora).  This is the shape of a model
  * layer's projections that read already-available inputs (q/k/v, GDN
  * qkv/z/b/a, gate/up, or the continuation GEMMs of one question). */
 typedef struct dq8_linear_item {
@@ -117,6 +145,7 @@ typedef struct dq8_linear_item {
     float *out;
     dq8_layout layout;
     dq8_epilogue epilogue;
+    const dq8_lora *lora; /* NULL: no adapter */
 } dq8_linear_item;
 dq8_status dq8_linear_batch(dq8_ctx *ctx, const dq8_linear_item *items_host, size_t count, void *stream);
 

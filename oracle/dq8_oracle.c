@@ -234,3 +234,107 @@ int dq8o_linear(const float *x, size_t rows, size_t width, const uint8_t *w, con
     free(q); free(xs); free(columns);
     return status;
 }
+
+/* -------------------------------------------------------------- LoRA (FP32) */
+
+/* dot_scores (tensor.rs:6-25), the x86-64 branch: eight partial sums, element i
+ * of every 8-element chunk going to lane i % 8 as `lane += a * b` (a rounded
+ * product, then a rounded add: Rust does not contract on x86-64); the lanes are
+ * summed in order by f32::sum, whose fold starts at -0.0; then the tail
+ * (len % 8 elements) is added one product at a time. */
+float dq8o_dot_scores(const float *a, const float *b, size_t len) {
+    size_t chunks = len / 8;
+    float lanes[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (size_t c = 0; c < chunks; ++c)
+        for (int i = 0; i < 8; ++i) {
+            float p = a[8 * c + i] * b[8 * c + i];
+            lanes[i] = lanes[i] + p;
+        }
+    float sum = -0.0f;
+    for (int i = 0; i < 8; ++i) sum = sum + lanes[i];
+    for (size_t t = 8 * chunks; t < len; ++t) {
+        float p = a[t] * b[t];
+        sum = sum + p;
+    }
+    return sum;
+}
+
+struct fctx {
+    const float *x; size_t rows; size_t width;
+    const float *w; const float *bias; float *columns;
+};
+/* The x86 FP32 columns (Projection::columns_tiled with T = 1, tensor.rs:206-269)
+ * without adapter: column j, row r = dot_scores(x_r, w_j) + bias[j], the bias
+ * being 0.0 when absent (tensor.rs:247-250). */
+static void fp32_columns_range(void *c, size_t b, size_t e) {
+    struct fctx *f = (struct fctx *)c;
+    for (size_t col = b; col < e; ++col) {
+        float bias = f->bias ? f->bias[col] : 0.0f;
+        for (size_t r = 0; r < f->rows; ++r)
+            f->columns[col * f->rows + r] = dq8o_dot_scores(f->x + r * f->width, f->w + col * f->width, f->width) + bias;
+    }
+}
+
+/* `linear` (tensor.rs:290-307) of an FP32 weight matrix w [outputs][width] with
+ * Epilogue::Write: result [rows][outputs].  Columns run in parallel when
+ * rows * outputs >= 512 (tensor.rs:254); results do not depend on it. */
+void dq8o_linear_f32(const float *x, size_t rows, size_t width, const float *w, size_t outputs, const float *bias,
+                     float *result, int threads) {
+    size_t nc = rows * outputs;
+    if (nc == 0) return;
+    float *columns = (float *)malloc(nc * sizeof(float));
+    if (!columns) return;
+    struct fctx c = {x, rows, width, w, bias, columns};
+    parallel_for(outputs, nc >= 512 ? threads : 1, fp32_columns_range, &c);
+    dq8o_write_columns(columns, rows, outputs, result, 0);
+    free(columns);
+}
+
+/* The LoRA middle product of Linear::apply_into_shared (weights.rs:480 and
+ * 495): mid [rows][rank] = linear(x, A) with A [rank][width], no bias. */
+void dq8o_lora_mid(const float *x, size_t rows, size_t width, const float *a, size_t rank, float *mid, int threads) {
+    dq8o_linear_f32(x, rows, width, a, rank, NULL, mid, threads);
+}
+
+/* Adapter::combine (tensor.rs:109-117): base + scale * (dot_scores(mid_row,
+ * b_row) + 0.0), the multiply and the add rounded separately. */
+float dq8o_lora_combine(float base, const float *mid_row, const float *b_row, size_t rank, float scale) {
+    float delta = dq8o_dot_scores(mid_row, b_row, rank) + 0.0f;
+    float scaled = scale * delta;
+    return base + scaled;
+}
+
+/* The x86 (non-SDOT) plan of Linear::apply_into_shared with a LoRA pair
+ * (weights.rs:450-491): values = linear(x, W, bias) (the int8 projection);
+ * mid = linear(x, A); delta = linear(mid, B); values[i] += scale * delta[i];
+ * then the epilogue stores values into result.  A is [rank][width] and B is
+ * [outputs][rank], both FP32.  Returns 1 where the reference falls back to FP32
+ * for the base projection (non-finite input), leaving `result` as is. */
+int dq8o_linear_lora(const float *x, size_t rows, size_t width, const uint8_t *w, const float *ws, size_t outputs,
+                     const float *bias, const float *a, const float *b, size_t rank, float scale, float *result,
+                     int epilogue, int threads) {
+    if (rows == 0) return 0;
+    size_t nv = rows * outputs, nm = rows * rank;
+    float *values = (float *)malloc((nv > 0 ? nv : 1) * sizeof(float));
+    float *mid = (float *)malloc((nm > 0 ? nm : 1) * sizeof(float));
+    float *delta = (float *)malloc((nv > 0 ? nv : 1) * sizeof(float));
+    int status = 2;
+    if (values && mid && delta) {
+        status = dq8o_linear(x, rows, width, w, ws, outputs, bias, values, 0, threads);
+        if (status == 0) {
+            dq8o_lora_mid(x, rows, width, a, rank, mid, threads);
+            dq8o_linear_f32(mid, rows, rank, b, outputs, NULL, delta, threads);
+            for (size_t i = 0; i < nv; ++i) {
+                float scaled = scale * delta[i];
+                values[i] = values[i] + scaled;
+            }
+            for (size_t i = 0; i < nv; ++i) {
+                if (epilogue == 0) result[i] = values[i];
+                else if (epilogue == 1) result[i] = result[i] + values[i];
+                else result[i] = dq8o_silu(result[i]) * values[i];
+            }
+        }
+    }
+    free(values); free(mid); free(delta);
+    return status;
+}

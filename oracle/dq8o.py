@@ -47,6 +47,17 @@ def lib():
         L.dq8o_write_columns.restype = None
         L.dq8o_linear.argtypes = [_f32p, _sz, _sz, _u8p, _f32p, _sz, ctypes.c_void_p, _f32p, ctypes.c_int, ctypes.c_int]
         L.dq8o_linear.restype = ctypes.c_int
+        L.dq8o_dot_scores.argtypes = [_f32p, _f32p, _sz]
+        L.dq8o_dot_scores.restype = ctypes.c_float
+        L.dq8o_linear_f32.argtypes = [_f32p, _sz, _sz, _f32p, _sz, ctypes.c_void_p, _f32p, ctypes.c_int]
+        L.dq8o_linear_f32.restype = None
+        L.dq8o_lora_mid.argtypes = [_f32p, _sz, _sz, _f32p, _sz, _f32p, ctypes.c_int]
+        L.dq8o_lora_mid.restype = None
+        L.dq8o_lora_combine.argtypes = [ctypes.c_float, _f32p, _f32p, _sz, ctypes.c_float]
+        L.dq8o_lora_combine.restype = ctypes.c_float
+        L.dq8o_linear_lora.argtypes = [_f32p, _sz, _sz, _u8p, _f32p, _sz, ctypes.c_void_p, _f32p, _f32p, _sz,
+                                       ctypes.c_float, _f32p, ctypes.c_int, ctypes.c_int]
+        L.dq8o_linear_lora.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -147,6 +158,66 @@ def linear(x, w, ws, bias=None, result=None, epilogue: int = 0, threads: int = 1
     out = np.zeros((rows, n), np.float32) if result is None else np.array(result, np.float32, copy=True, order="C")
     keep, bp = _bias_ptr(bias)
     st = lib().dq8o_linear(x, rows, k, w, ws, n, bp, out, epilogue, threads)
+    if st == 1:
+        return None
+    if st != 0:
+        raise MemoryError("oracle allocation failed")
+    return out
+
+
+def dot_scores(a, b) -> np.float32:
+    """dot_scores (tensor.rs:6-25), x86-64 order."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    assert a.shape == b.shape and a.ndim == 1
+    return np.float32(lib().dq8o_dot_scores(a, b, a.size))
+
+
+def linear_f32(x, w, bias=None, threads: int = 1) -> np.ndarray:
+    """`linear` of FP32 weights w [N][K] (Epilogue::Write): result [M][N]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, k = x.shape
+    n = w.shape[0]
+    out = np.zeros((rows, n), np.float32)
+    keep, bp = _bias_ptr(bias)
+    lib().dq8o_linear_f32(x, rows, k, w, n, bp, out, threads)
+    return out
+
+
+def lora_mid(x, a, threads: int = 1) -> np.ndarray:
+    """LoRA middle product mid [M][rank] = linear(x, A), A [rank][K]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    rows, k = x.shape
+    rank = a.shape[0]
+    mid = np.zeros((rows, rank), np.float32)
+    lib().dq8o_lora_mid(x, rows, k, a, rank, mid, threads)
+    return mid
+
+
+def lora_combine(base: float, mid_row, b_row, scale: float) -> np.float32:
+    """Adapter::combine (tensor.rs:109-117)."""
+    mid_row = np.ascontiguousarray(mid_row, dtype=np.float32)
+    b_row = np.ascontiguousarray(b_row, dtype=np.float32)
+    return np.float32(lib().dq8o_lora_combine(float(base), mid_row, b_row, mid_row.size, float(scale)))
+
+
+def linear_lora(x, w, ws, a, b, scale: float, bias=None, result=None, epilogue: int = 0, threads: int = 1):
+    """The x86 plan of Linear::apply_into with a LoRA pair (A [rank][K], B [N][rank],
+    FP32): result [M][N], or None when the base projection would fall back to FP32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    ws = np.ascontiguousarray(ws, dtype=np.float32)
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    rows, k = x.shape
+    n = w.shape[0]
+    rank = a.shape[0]
+    assert a.shape == (rank, k) and b.shape == (n, rank)
+    out = np.zeros((rows, n), np.float32) if result is None else np.array(result, np.float32, copy=True, order="C")
+    keep, bp = _bias_ptr(bias)
+    st = lib().dq8o_linear_lora(x, rows, k, w, ws, n, bp, a, b, rank, float(scale), out, epilogue, threads)
     if st == 1:
         return None
     if st != 0:

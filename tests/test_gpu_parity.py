@@ -304,3 +304,139 @@ def test_config1_single_linear_seed0_bit_exact(ctx):
     assert np.array_equal(host(ev), wv) and bits_equal(host(es), ws)
     assert np.array_equal(dots, dq8o.group_dots(qh, wv))
     assert bits_equal(out, dq8o.linear(x, wv, ws, threads=8))
+
+
+# ------------------------------------------------------------------- LoRA
+
+LORA_MID_SHAPES = [(1, 64, 1), (5, 131, 13), (24, 2048, 16), (67, 100, 3), (130, 2048, 16), (9, 7, 9), (4, 6144, 8)]
+
+
+@pytest.mark.parametrize("m,k,rank", LORA_MID_SHAPES)
+def test_lora_mid_bit_exact(ctx, m, k, rank):
+    rng = np.random.default_rng(m * 7 + k + rank)
+    x = make_x(rng, m, k)
+    a = (rng.standard_normal((rank, k)) * 0.05).astype(np.float32)
+    got = host(ctx.lora_mid(dev(x), dev(a)))
+    assert bits_equal(got, dq8o.lora_mid(x, a, threads=4))
+
+
+# (m, k, n, rank): skinny (m <= 32, short and long K) and wide kernels; ranks
+# with full chunks of 8, tails, both, and rank 0.
+LORA_SHAPES = [(1, 64, 4, 3), (5, 131, 31, 13), (24, 2048, 96, 16), (17, 6144, 40, 8), (32, 256, 70, 1),
+               (67, 131, 31, 13), (130, 2048, 100, 16), (64, 192, 65, 24), (19, 128, 9, 0)]
+
+
+def _lora_case(rng, m, k, n, rank):
+    x = make_x(rng, m, k)
+    wv, ws = dq8o.quantize_weights(make_w(rng, n, k))
+    a = (rng.standard_normal((rank, k)) * 0.05).astype(np.float32)
+    b = (rng.standard_normal((n, rank)) * 0.05).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    return x, wv, ws, a, b, bias
+
+
+@pytest.mark.parametrize("m,k,n,rank", LORA_SHAPES)
+def test_linear_lora_bit_exact(ctx, m, k, n, rank):
+    rng = np.random.default_rng(m * 31 + k + n * 3 + rank)
+    x, wv, ws, a, b, bias = _lora_case(rng, m, k, n, rank)
+    scale = 0.375
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    mid = ctx.lora_mid(dev(x), dev(a))
+    lora = dq8.Lora(mid, dev(b), scale)
+    want = dq8o.linear_lora(x, wv, ws, a, b, scale, bias=bias, threads=4)
+    got = host(ctx.linear_lora(h, q, s, lora, bias=dev(bias)))
+    assert bits_equal(got, want)
+    # Add epilogue and the column layout (linear_int8's own return, tensor.rs:438)
+    base = rng.standard_normal((m, n)).astype(np.float32)
+    out = dev(base.copy())
+    ctx.linear_lora(h, q, s, lora, out=out, bias=dev(bias), epilogue=dq8.ADD)
+    assert bits_equal(host(out), dq8o.linear_lora(x, wv, ws, a, b, scale, bias=bias, result=base, epilogue=1))
+    cols = host(ctx.linear_lora(h, q, s, lora, bias=dev(bias), layout=dq8.COLUMNS))
+    assert bits_equal(cols, np.ascontiguousarray(want.T))
+
+
+def test_linear_lora_swiglu_epilogue(ctx):
+    rng = np.random.default_rng(11)
+    m, k, n, rank = 24, 2048, 96, 16
+    x, wv, ws, a, b, bias = _lora_case(rng, m, k, n, rank)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    lora = dq8.Lora(ctx.lora_mid(dev(x), dev(a)), dev(b), 2.0)
+    gate = (rng.standard_normal((m, n)) * 3).astype(np.float32)
+    out = dev(gate.copy())
+    ctx.linear_lora(h, q, s, lora, out=out, bias=dev(bias), epilogue=dq8.SWIGLU)
+    want = dq8o.linear_lora(x, wv, ws, a, b, 2.0, bias=bias, result=gate, epilogue=2)
+    got = host(out)
+    rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
+    assert float(rel.max()) <= SWIGLU_RTOL
+
+
+@pytest.mark.parametrize("rows", [1, 19, 67])
+def test_reference_fused_lora_case(ctx, rows):
+    # weights.rs:657-706: input 131, output 31, rank 13, scale 0.375, bf16-valued
+    # weights and LoRA matrices, a bias; Write, Add and SwiGlu.
+    width, output, rank, scale = 131, 31, 13, 0.375
+    x = np.array([((i * 43 % 113) - 56.0) / 32.0 for i in range(rows * width)], np.float32).reshape(rows, width)
+
+    def packed(count):
+        v = np.array([((i * 17 % 89) - 44.0) / 32.0 for i in range(count)], np.float32)
+        return (v.view(np.uint32) & 0xFFFF0000).view(np.float32)
+    wv, ws = dq8o.quantize_weights(packed(output * width).reshape(output, width))
+    a = packed(rank * width).reshape(rank, width)
+    b = packed(output * rank).reshape(output, rank)
+    bias = np.array([i / 64.0 - 0.25 for i in range(output)], np.float32)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    lora = dq8.Lora(ctx.lora_mid(dev(x), dev(a)), dev(b), scale)
+    expected = dq8o.linear_lora(x, wv, ws, a, b, scale, bias=bias)
+    assert bits_equal(host(ctx.linear_lora(h, q, s, lora, bias=dev(bias))), expected)
+    original = np.array([i / 16.0 - 3.0 for i in range(rows * output)], np.float32).reshape(rows, output)
+    out = dev(original.copy())
+    ctx.linear_lora(h, q, s, lora, out=out, bias=dev(bias), epilogue=dq8.ADD)
+    assert bits_equal(host(out), (original + expected).astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,width,output", [(1, 64, 4), (4, 64, 4), (5, 128, 6), (9, 192, 31), (67, 128, 8),
+                                               (7, 100, 9)])
+def test_reference_adapter_tile_case(ctx, rows, width, output):
+    # tensor.rs:664-732: the projection with a rank-3 adapter whose middle
+    # product is given; every output = Adapter::combine(scaled_dot + bias).
+    rank = 3
+    groups = -(-width // 64)
+    x = np.array([((i * 43 % 255) - 127.0) / 9.0 for i in range(rows * width)], np.float32).reshape(rows, width)
+    values = np.array([(i * 71 + 128) & 0xFF for i in range(output * width)], np.uint8).reshape(output, width)
+    scales = np.array([(i % 7 + 1) / 32.0 for i in range(output * groups)], np.float32).reshape(output, groups)
+    bias = np.array([i / 16.0 - 0.5 for i in range(output)], np.float32)
+    mid = np.array([(i % 9) / 4.0 - 1.0 for i in range(rows * rank)], np.float32).reshape(rows, rank)
+    bw = np.array([(i % 7) / 8.0 for i in range(output * rank)], np.float32).reshape(output, rank)
+    h = ctx.weights_from_quantized(dev(values), dev(scales))
+    q, s = ctx.quantize(dev(x))
+    got = host(ctx.linear_lora(h, q, s, dq8.Lora(dev(mid), dev(bw), 0.375), bias=dev(bias)))
+    qh, sh = dq8o.quantize_inputs(x)
+    for column in range(output):
+        for row in range(rows):
+            base = np.float32(dq8o.scaled_dot(qh[row], sh[row], values[column], scales[column]) + bias[column])
+            want = dq8o.lora_combine(base, mid[row], bw[column], 0.375)
+            assert got[row, column].tobytes() == np.float32(want).tobytes()
+
+
+def test_linear_batch_with_and_without_lora(ctx):
+    rng = np.random.default_rng(5)
+    items, wants = [], []
+    for (m, k, n, rank) in [(24, 2048, 96, 16), (24, 2048, 40, 0), (24, 6144, 33, 8), (70, 256, 64, 16),
+                            (70, 256, 40, None)]:
+        x, wv, ws, a, b, bias = _lora_case(rng, m, k, n, rank or 0)
+        h = ctx.weights_from_quantized(dev(wv), dev(ws))
+        q, s = ctx.quantize(dev(x))
+        out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+        if rank is None:
+            items.append(dq8.Item(h, q, s, out, bias=dev(bias)))
+            wants.append(dq8o.linear(x, wv, ws, bias=bias, threads=4))
+        else:
+            lora = dq8.Lora(ctx.lora_mid(dev(x), dev(a)), dev(b), -1.5)
+            items.append(dq8.Item(h, q, s, out, bias=dev(bias), lora=lora))
+            wants.append(dq8o.linear_lora(x, wv, ws, a, b, -1.5, bias=bias, threads=4))
+    ctx.linear_batch(items)
+    for it, want in zip(items, wants):
+        assert bits_equal(host(it.out), want)

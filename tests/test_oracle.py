@@ -338,3 +338,164 @@ def test_planted_rounding_and_transpose_faults_are_detected():
     right = dq8o.group_dots(qx, values)
     wrong = onp.group_dots(qx, np.ascontiguousarray(values.reshape(128, 6).T))
     assert not np.array_equal(right, wrong)
+
+
+# ------------------------------------------------------------ LoRA (FP32)
+
+def py_dot_scores(a, b):
+    """Scalar emulation of dot_scores (tensor.rs:6-25, x86-64): eight lanes of
+    `lane += a * b`, summed in order from -0.0, then the tail one product at a time."""
+    n = len(a)
+    chunks = n // 8
+    lanes = [0.0] * 8
+    for c in range(chunks):
+        for i in range(8):
+            lanes[i] = f32(lanes[i] + f32(float(a[8 * c + i]) * float(b[8 * c + i])))
+    s = -0.0
+    for i in range(8):
+        s = f32(s + lanes[i])
+    for t in range(8 * chunks, n):
+        s = f32(s + f32(float(a[t]) * float(b[t])))
+    return s
+
+
+def test_dot_scores_lane_structure_and_tail_order_known_answers():
+    # Lane i holds elements i, i+8, ...: 1e8 and -1e8 in lane 0 cancel before
+    # the lane sum adds lane 1's 1.0 -> 1.0.  A sequential sum would absorb the
+    # 1.0 into 1e8 and return 0.0.
+    a = np.zeros(16, np.float32); a[0], a[8], a[1] = 1e8, -1e8, 1.0
+    assert dq8o.dot_scores(a, np.ones(16, np.float32)) == 1.0
+    # The tail (elements past the last full chunk) is added after the lane sum:
+    # (1 + 1e8) - 1e8 = 0.0 in binary32; tail-first order would give 1.0.
+    a = np.zeros(10, np.float32); a[0], a[8], a[9] = 1.0, 1e8, -1e8
+    assert dq8o.dot_scores(a, np.ones(10, np.float32)) == 0.0
+    # Products are rounded before the add (no fused multiply-add): with
+    # a = b = 1 + 2^-12, a*b = 1 + 2^-11 + 2^-24 rounds to 1 + 2^-11 (tie to
+    # even), so lane + a*b - (1 + 2^-11) is exactly 0; an FMA would keep 2^-24.
+    e = np.float32(1 + 2.0 ** -12)
+    a = np.array([e] + [0] * 7 + [-1.0] + [0] * 7, np.float32)
+    b = np.array([e] + [0] * 7 + [1 + 2.0 ** -11] + [0] * 7, np.float32)
+    assert dq8o.dot_scores(a, b) == 0.0
+    assert dq8o.dot_scores(np.zeros(0, np.float32), np.zeros(0, np.float32)) == 0.0
+
+
+@pytest.mark.parametrize("length", list(range(0, 41)) + [63, 64, 65, 131, 2048])
+def test_dot_scores_integer_vectors_are_exact(length):
+    # Small integers: every partial sum is exact, so any grouping must give the
+    # integer dot product (a dropped or doubled term fails).
+    a = np.array([(i * 37 % 19) - 9 for i in range(length)], np.float32)
+    b = np.array([(i * 11 % 13) - 6 for i in range(length)], np.float32)
+    assert float(dq8o.dot_scores(a, b)) == float(sum(int(x) * int(y) for x, y in zip(a, b)))
+
+
+@pytest.mark.parametrize("length", [0, 1, 7, 8, 9, 15, 16, 17, 40, 63, 64, 65, 131])
+def test_dot_scores_matches_scalar_emulation_on_special_values(length):
+    # The value mix of tensor.rs:806-829 (-0.0, 1e-30, -3.5e8 and fractions).
+    def v(seed):
+        out = []
+        for i in range(length):
+            k = (i + seed) % 11
+            out.append(-0.0 if k == 0 else 1e-30 if k == 1 else -3.5e8 if k == 2
+                       else ((i * 37 + seed * 101) % 997) / 61.0 - 8.0 + k / 7.0)
+        return np.array(out, np.float32)
+    a, b = v(1), v(2)
+    got = dq8o.dot_scores(a, b)
+    assert np.float32(got).tobytes() == np.float32(py_dot_scores(a, b)).tobytes()
+
+
+def test_dot_scores_within_fp64_bound():
+    rng = np.random.default_rng(7)
+    for n in [16, 100, 2048]:
+        a = rng.standard_normal(n).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        exact = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
+        bound = (n + 2) * 2.0 ** -24 * float(np.sum(np.abs(a.astype(np.float64) * b)))
+        assert abs(float(dq8o.dot_scores(a, b)) - exact) <= bound
+
+
+def test_lora_combine_known_answers():
+    # rank 3 is tail-only: 1*1 + 2*1 + 3*1 = 6; 1 + 0.375 * (6 + 0.0) = 3.25
+    assert dq8o.lora_combine(1.0, [1.0, 2.0, 3.0], [1.0, 1.0, 1.0], 0.375) == 3.25
+    # + 0.0 turns a -0.0 delta into +0.0, so -0.0 + scale * delta is +0.0
+    r = dq8o.lora_combine(-0.0, [-0.0], [1.0], 2.0)
+    assert r == 0.0 and np.float32(r).tobytes() == np.float32(0.0).tobytes()
+
+
+@pytest.mark.parametrize("rows,width,output", [(1, 64, 4), (4, 64, 4), (5, 128, 6), (9, 192, 31), (67, 128, 8),
+                                               (7, 100, 9)])
+def test_projection_with_adapter_matches_per_output_combine(rows, width, output):
+    # tensor.rs:664-732 with its rank-3 adapter: the x86 plan of the oracle equals
+    # scaled_dot + bias, then Adapter::combine, per output, bitwise.  The middle
+    # product is the test's own `mid`, so it enters through an identity A.
+    rank = 3
+    groups = -(-width // 64)
+    x = np.array([((i * 43 % 255) - 127.0) / 9.0 for i in range(rows * width)], np.float32).reshape(rows, width)
+    values = np.array([(i * 71 + 128) & 0xFF for i in range(output * width)], np.uint8).reshape(output, width)
+    scales = np.array([(i % 7 + 1) / 32.0 for i in range(output * groups)], np.float32).reshape(output, groups)
+    bias = np.array([i / 16.0 - 0.5 for i in range(output)], np.float32)
+    mid = np.array([(i % 9) / 4.0 - 1.0 for i in range(rows * rank)], np.float32).reshape(rows, rank)
+    bw = np.array([(i % 7) / 8.0 for i in range(output * rank)], np.float32).reshape(output, rank)
+    q, xs = dq8o.quantize_inputs(x)
+    for column in range(output):
+        for row in range(rows):
+            base = np.float32(dq8o.scaled_dot(q[row], xs[row], values[column], scales[column]) + bias[column])
+            want = dq8o.lora_combine(base, mid[row], bw[column], 0.375)
+            # the same combine written out: base + scale * (dot_scores + 0.0)
+            alt = np.float32(base + np.float32(np.float32(0.375) * np.float32(py_dot_scores(mid[row], bw[column]) + 0.0)))
+            assert np.float32(want).tobytes() == alt.tobytes()
+
+
+@pytest.mark.parametrize("rows", [1, 19, 67])
+def test_fused_lora_matches_separate_projections(rows):
+    # weights.rs:657-706: the fused plan equals base + scale * delta computed by
+    # separate projections, for Write, Add and SwiGlu.
+    width, output, rank, scale = 131, 31, 13, 0.375
+    x = np.array([((i * 43 % 113) - 56.0) / 32.0 for i in range(rows * width)], np.float32).reshape(rows, width)
+
+    def packed(count):  # bf16-valued weights, as the reference test packs them
+        v = np.array([((i * 17 % 89) - 44.0) / 32.0 for i in range(count)], np.float32)
+        return (v.view(np.uint32) & 0xFFFF0000).view(np.float32)
+    wv, ws = dq8o.quantize_weights(packed(output * width).reshape(output, width))
+    a = packed(rank * width).reshape(rank, width)
+    b = packed(output * rank).reshape(output, rank)
+    bias = np.array([i / 64.0 - 0.25 for i in range(output)], np.float32)
+    base = dq8o.linear(x, wv, ws, bias=bias)
+    mid = dq8o.linear_f32(x, a)
+    delta = dq8o.linear_f32(mid, b)
+    expected = (base + (np.float32(scale) * delta).astype(np.float32)).astype(np.float32)
+    got = dq8o.linear_lora(x, wv, ws, a, b, scale, bias=bias, threads=4)
+    assert got.tobytes() == expected.tobytes()
+    original = np.array([i / 16.0 - 3.0 for i in range(rows * output)], np.float32).reshape(rows, output)
+    add = dq8o.linear_lora(x, wv, ws, a, b, scale, bias=bias, result=original, epilogue=1)
+    assert add.tobytes() == (original + expected).astype(np.float32).tobytes()
+    sw = dq8o.linear_lora(x, wv, ws, a, b, scale, bias=bias, result=original, epilogue=2)
+    want = np.array([dq8o.silu(o) * e for o, e in zip(original.ravel(), expected.ravel())], np.float32)
+    assert sw.ravel().tobytes() == want.tobytes()
+
+
+def test_lora_mid_is_linear_of_a_and_scale_zero_leaves_base():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((5, 200)).astype(np.float32)
+    a = rng.standard_normal((16, 200)).astype(np.float32)
+    mid = dq8o.lora_mid(x, a)
+    for r in range(5):
+        for j in range(16):
+            assert np.float32(mid[r, j]).tobytes() == np.float32(py_dot_scores(x[r], a[j]) + 0.0).tobytes()
+    wv, ws = dq8o.quantize_weights(rng.standard_normal((9, 200)).astype(np.float32) * 0.02)
+    b = rng.standard_normal((9, 16)).astype(np.float32)
+    base = dq8o.linear(x, wv, ws)
+    assert dq8o.linear_lora(x, wv, ws, a, b, 0.0).tobytes() == (base + np.float32(0.0)).astype(np.float32).tobytes()
+
+
+def test_planted_dot_scores_faults_are_detected():
+    # Sequential summation or a fused multiply-add must fail the known answers above.
+    def sequential(a, b):
+        s = 0.0
+        for x, y in zip(a, b):
+            s = f32(s + f32(float(x) * float(y)))
+        return s
+    a = np.zeros(16, np.float32); a[0], a[8], a[1] = 1e8, -1e8, 1.0
+    assert sequential(a, np.ones(16, np.float32)) != 1.0
+    e = 1 + 2.0 ** -12
+    fused = f32(e * e - (1 + 2.0 ** -11))  # what an FMA would leave in lane 0
+    assert fused != 0.0
