@@ -25,6 +25,7 @@ reference's x86 path) on a bounded sample of the same workload.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -51,6 +52,8 @@ def parse():
     p.add_argument("--skinny-reps", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--lora-rank", type=int, default=16,
+                   help="rank of the LoRA adapters of the stack's second pass (0: skip it)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device copy (for rocprof counter calibration)")
     return p.parse_args()
@@ -136,30 +139,79 @@ def main():
         return ("linear", lib.dq8_linear, (ctx.handle, w.handle, q.data_ptr(), s.data_ptr(), M, None,
                                            out.data_ptr(), dq8.ROWS, ep, sh), (0, 2 * M * w.n * w.k))
 
-    calls = []
-    for L in layers:
-        calls.append(quant(L["x"], qx, sx, HIDDEN))
-        if L["kind"] == "gdn":
-            calls.append(linear(L["in"], qx, sx, mixer_out, dq8.WRITE))
-        else:
-            items = (dq8._Item * 3)()
-            outs = (mixer_out, k_out, v_out)
-            for i, name in enumerate(("q", "k", "v")):
-                items[i] = dq8._Item(L[name].handle, qx.data_ptr(), sx.data_ptr(), M, None, outs[i].data_ptr(),
-                                     dq8.ROWS, dq8.WRITE)
-            L["items"] = items
-            flops = sum(2 * M * L[n].n * L[n].k for n in ("q", "k", "v"))
-            calls.append(("linear", lib.dq8_linear_batch, (ctx.handle, items, 3, sh), (0, flops)))
-        calls.append(quant(L["mix"], qx, sx, HIDDEN))
-        calls.append(linear(L["out"] if L["kind"] == "gdn" else L["o"], qx, sx, proj_out, dq8.WRITE))
-        calls.append(quant(L["ffn"], qx, sx, HIDDEN))
-        calls.append(linear(L["gate"], qx, sx, gate, dq8.WRITE))
-        calls.append(linear(L["up"], qx, sx, gate, dq8.SWIGLU))
-        calls.append(quant(gate, qf, sf, FFN_DIM))
-        calls.append(linear(L["down"], qf, sf, resid, dq8.ADD))
+    rank = args.lora_rank
+    mids = {k: torch.empty((M, max(rank, 1)), dtype=torch.float32, device=dev) for k in ("a", "b", "c")}
+    keep = []  # ctypes structs referenced by queued calls
+
+    def lora_of(L, name):
+        """The projection's rank-`rank` FP32 LoRA pair (A [rank][K], B [N][rank]), made on first use."""
+        key = "lora_" + name
+        if key not in L:
+            w = L[name]
+            a = (torch.randn((rank, w.k), generator=gen, device=dev) * 0.02).contiguous()
+            b = (torch.randn((w.n, rank), generator=gen, device=dev) * 0.02).contiguous()
+            L[key] = (a, b)
+        return L[key]
+
+    def mid_call(x, a, mid, k):
+        return ("mid", lib.dq8_lora_mid, (ctx.handle, x.data_ptr(), M, k, a.data_ptr(), rank, mid.data_ptr(), sh),
+                (0, 2 * M * k * rank))
+
+    def lora_linear(L, name, x, q, s, out, ep, mid, k):
+        """mid = linear(x, A) then the projection with its adapter (weights.rs:492-520)."""
+        a, b = lora_of(L, name)
+        w = L[name]
+        lo = dq8._Lora(mid.data_ptr(), b.data_ptr(), rank, 2.0)
+        keep.append(lo)
+        return [mid_call(x, a, mid, k),
+                ("linear", lib.dq8_linear_lora, (ctx.handle, w.handle, q.data_ptr(), s.data_ptr(), M, None,
+                                                 ctypes.byref(lo), out.data_ptr(), dq8.ROWS, ep, sh),
+                 (0, 2 * M * w.n * w.k))]
+
+    def build(with_lora):
+        calls = []
+
+        def proj(L, name, x, q, s, out, ep, mid, k):
+            if with_lora:
+                calls.extend(lora_linear(L, name, x, q, s, out, ep, mid, k))
+            else:
+                calls.append(linear(L[name], q, s, out, ep))
+
+        for L in layers:
+            calls.append(quant(L["x"], qx, sx, HIDDEN))
+            if L["kind"] == "gdn":
+                proj(L, "in", L["x"], qx, sx, mixer_out, dq8.WRITE, mids["a"], HIDDEN)
+            else:
+                items = (dq8._Item * 3)()
+                outs = (mixer_out, k_out, v_out)
+                for i, name in enumerate(("q", "k", "v")):
+                    lp = None
+                    if with_lora:
+                        a, b = lora_of(L, name)
+                        mid = torch.empty((M, rank), dtype=torch.float32, device=dev)
+                        keep.append(mid)
+                        calls.append(mid_call(L["x"], a, mid, HIDDEN))
+                        lo = dq8._Lora(mid.data_ptr(), b.data_ptr(), rank, 2.0)
+                        keep.append(lo)
+                        lp = ctypes.pointer(lo)
+                    items[i] = dq8._Item(L[name].handle, qx.data_ptr(), sx.data_ptr(), M, None, outs[i].data_ptr(),
+                                         dq8.ROWS, dq8.WRITE, lp)
+                keep.append(items)
+                flops = sum(2 * M * L[n].n * L[n].k for n in ("q", "k", "v"))
+                calls.append(("linear", lib.dq8_linear_batch, (ctx.handle, items, 3, sh), (0, flops)))
+            calls.append(quant(L["mix"], qx, sx, HIDDEN))
+            proj(L, "out" if L["kind"] == "gdn" else "o", L["mix"], qx, sx, proj_out, dq8.WRITE, mids["a"], HIDDEN)
+            calls.append(quant(L["ffn"], qx, sx, HIDDEN))
+            proj(L, "gate", L["ffn"], qx, sx, gate, dq8.WRITE, mids["b"], HIDDEN)
+            proj(L, "up", L["ffn"], qx, sx, gate, dq8.SWIGLU, mids["c"], HIDDEN)
+            calls.append(quant(gate, qf, sf, FFN_DIM))
+            proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
+        return calls
+
+    calls = build(False)
     step_ops = sum(c[3][1] for c in calls)
 
-    def run_step(events=None):
+    def run_step(events=None, calls=calls):
         for i, (kind, fn, a, _) in enumerate(calls):
             if events is not None:
                 events[i][0].record(stream)
@@ -202,6 +254,7 @@ def main():
     lin_avg_ms = lin_ms / lin_n
     achieved = lin_ops_per_launch / (lin_avg_ms * 1e-3) / 1e12
     value = step_ops / (ms_step * 1e-3) / 1e12
+    lora = run_lora_stack(args, torch, stream, build, run_step, step_ops, ms_step) if rank > 0 else None
 
     # release the stack before the skinny workload
     for L in layers:
@@ -251,9 +304,42 @@ def main():
             "avg_launch_ms": round(lin_avg_ms, 5),
         },
         "skinny": skinny,
+        "lora": lora,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
+
+
+def run_lora_stack(args, torch, stream, build, run_step, step_ops, base_ms):
+    """The same stack with a rank-r FP32 LoRA pair on every projection, as the
+    reference's checkpoints carry (weights.rs:420-424): per projection the middle
+    product mid = x.A^T (dq8_lora_mid) and the projection with its adapter."""
+    calls = build(True)
+    for _ in range(2):
+        run_step(calls=calls)
+    torch.cuda.synchronize()
+    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in calls]
+          for _ in range(args.steps)]
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for s in range(args.steps):
+        run_step(ev[s], calls=calls)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / args.steps
+    mid_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(args.steps)
+                 for i, c in enumerate(calls) if c[0] == "mid") / args.steps
+    lin_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(args.steps)
+                 for i, c in enumerate(calls) if c[0] == "linear") / args.steps
+    return {
+        "workload": f"the stack above with a rank-{args.lora_rank} FP32 LoRA pair on every projection",
+        "rank": args.lora_rank,
+        "ms_per_step": round(ms_step, 4),
+        "tops_base_ops": round(step_ops / (ms_step * 1e-3) / 1e12, 2),
+        "overhead_vs_base": round(ms_step / base_ms - 1.0, 4),
+        "mid_ms_per_step": round(mid_ms, 4),
+        "projection_ms_per_step": round(lin_ms, 4),
+    }
 
 
 def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):

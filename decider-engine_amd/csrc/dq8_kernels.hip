@@ -42,6 +42,11 @@ __device__ __forceinline__ v16i mfma_i8(v4i a, v4i b, v16i c) {
 __device__ __forceinline__ v32f mfma_k1(float a, float b, v32f c) {
   return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
 }
+// One 32x32 block with K=2: lanes 0-31 carry k=0 (row / column l), lanes 32-63
+// k=1.  With the k=1 operands zero it is the K=1 outer product of one block.
+__device__ __forceinline__ v16f mfma_k2(float a, float b, v16f c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ v32f concat(v16i lo, v16i hi) {
   v16f a = __builtin_bit_cast(v16f, lo), b = __builtin_bit_cast(v16f, hi);
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20,
@@ -113,6 +118,29 @@ __device__ __forceinline__ V lora_term(const V& base, const V& zero, int rank, f
     }
   }
   for (int t = 8 * chunks; t < rank; ++t) sum = sum + prod(t);
+  return base + scale * (sum + zero);
+}
+
+// lora_term for rank <= 16 with every index a compile-time constant after
+// unrolling, so the operands can sit in registers, loaded up front.
+template <typename V, typename Prod>
+__device__ __forceinline__ V lora_term16(const V& base, const V& zero, int rank, float scale, Prod prod) {
+  const int chunks = rank >> 3;
+  V sum = zero;
+  if (chunks > 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      V ln = prod(i);
+      if (chunks > 1) ln = ln + prod(8 + i);
+      sum = i == 0 ? ln : sum + ln;
+      __builtin_amdgcn_sched_barrier(0);  // keeps the products of one lane live at a time
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 16; ++t) {
+    if (t >= 8 * chunks && t < rank) sum = sum + prod(t);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   return base + scale * (sum + zero);
 }
 
@@ -392,9 +420,9 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   struct XChunk {
     uint8_t d[XD][kFragBytes];
   };
-  __shared__ __attribute__((aligned(16))) Stage st0, st1, st2, st3;
+  __shared__ __attribute__((aligned(16))) Stage stg[STAGES];
   __shared__ __attribute__((aligned(16))) XChunk xc[DOTS ? 1 : 2];
-  auto stage = [&](int i) -> Stage& { return i == 0 ? st0 : i == 1 ? st1 : i == 2 ? st2 : st3; };
+  auto stage = [&](int i) -> Stage& { return stg[i]; };
 
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -571,14 +599,65 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 #pragma unroll
       for (int v = 0; v < 32; ++v) s[j][v] = s[j][v] + bias[RT == 2 ? j : v >> 4];
     if (LORA && P.lora) {
-      // then + scale * (mid . b + 0.0) (tensor.rs:438, 109-117); the K=1 MFMA
-      // operands follow the x/w scale convention of the group loop.
-      const float* lm = P.lmid + (size_t)min(mw + (RT == 2 ? lane : (lane & 31)), P.m - 1) * P.rank;
+      // then + scale * (mid . b + 0.0) (tensor.rs:438, 109-117), one 32x32
+      // block at a time: block b of pair j is row tile b (RT == 2) or column
+      // tile b (RT == 1); products from a K=2 MFMA whose k=1 operands (lanes
+      // 32-63) are zero.  For rank <= 16 the wave first copies its mid rows and
+      // b columns into the (now idle) LDS ring, rows padded to 17 floats so the
+      // operand reads hit distinct banks; the products then wait on LDS, not L2.
+      v16f zero16;
 #pragma unroll
-      for (int j = 0; j < NP; ++j) {
-        const float* lbc = P.lb + (size_t)min(nw + (RT == 2 ? 32 * j + (lane & 31) : lane), P.n - 1) * P.rank;
-        s[j] = lora_term(s[j], zero32, P.rank, P.lscale, [&](int i) { return mfma_k1(lm[i], lbc[i], zero32); });
+      for (int i = 0; i < 16; ++i) zero16[i] = 0.0f;
+      const bool k0 = lane < 32;
+      // Operand rows of 16 floats, element i of row r at r*16 + (i ^ ((r >> 2) & 15)):
+      // the 32 lanes reading one element of 32 consecutive rows hit 32 banks.
+      constexpr int WROWS = 32 * RT, WCOLS = 32 * CT, LWAVE = (WROWS + WCOLS) * 16 * 4;
+      constexpr bool FITS = NW * LWAVE <= STAGES * (int)sizeof(Stage);
+      const bool staged = FITS && P.rank <= 16;
+      float* lmid = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(&stg[0]) + wid * LWAVE);
+      float* lbw = lmid + WROWS * 16;
+      auto sw = [](int r, int i) { return r * 16 + (i ^ ((r >> 2) & 15)); };
+      if (staged) {
+        lds_barrier();  // every wave is done reading the ring
+        // all loads first (one memory latency), then the LDS writes
+        static_assert(WROWS <= 64 && WCOLS <= 64, "one row and one column per lane");
+        const float* gm = P.lmid + (size_t)min(mw + (lane % WROWS), P.m - 1) * P.rank;
+        const float* gb = P.lb + (size_t)min(nw + (lane % WCOLS), P.n - 1) * P.rank;
+        float vm[16], vb[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          vm[i] = i < P.rank ? gm[i] : 0.0f;
+          vb[i] = i < P.rank ? gb[i] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (lane < WROWS) lmid[sw(lane, i)] = vm[i];
+          if (lane < WCOLS) lbw[sw(lane, i)] = vb[i];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's copies are visible to it
       }
+#pragma unroll
+      for (int j = 0; j < NP; ++j)
+#pragma unroll
+        for (int bk = 0; bk < 2; ++bk) {
+          const int r = (RT == 2 ? 32 * bk : 0) + (lane & 31);
+          const int c = (RT == 2 ? 32 * j : 32 * bk) + (lane & 31);
+          v16f base;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) base[v] = s[j][16 * bk + v];
+          if (staged) {
+            base = lora_term(base, zero16, P.rank, P.lscale, [&](int i) {
+              return mfma_k2(k0 ? lmid[sw(r, i)] : 0.0f, k0 ? lbw[sw(c, i)] : 0.0f, zero16);
+            });
+          } else {
+            const float* lm = P.lmid + (size_t)min(mw + r, P.m - 1) * P.rank;
+            const float* lbc = P.lb + (size_t)min(nw + c, P.n - 1) * P.rank;
+            base = lora_term(base, zero16, P.rank, P.lscale,
+                             [&](int i) { return mfma_k2(k0 ? lm[i] : 0.0f, k0 ? lbc[i] : 0.0f, zero16); });
+          }
+#pragma unroll
+          for (int v = 0; v < 16; ++v) s[j][16 * bk + v] = base[v];
+        }
     }
     constexpr int E = NP * 32;
     int rows[E], cols[E];
@@ -692,8 +771,19 @@ __device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, v4
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         const float* lbc = P.lb + (size_t)min(c0 + 16 * ct + (lane & 15), P.n - 1) * P.rank;
-        s[rt * CT + ct] = lora_term(s[rt * CT + ct], zero4, P.rank, P.lscale,
-                                    [&](int i) { return mfma_k1_4(lm[i], lbc[i], zero4); });
+        if (P.rank <= 16) {
+          float am[16], bm[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            am[i] = i < P.rank ? lm[i] : 0.0f;
+            bm[i] = i < P.rank ? lbc[i] : 0.0f;
+          }
+          s[rt * CT + ct] = lora_term16(s[rt * CT + ct], zero4, P.rank, P.lscale,
+                                        [&](int i) { return mfma_k1_4(am[i], bm[i], zero4); });
+        } else {
+          s[rt * CT + ct] = lora_term(s[rt * CT + ct], zero4, P.rank, P.lscale,
+                                      [&](int i) { return mfma_k1_4(lm[i], lbc[i], zero4); });
+        }
       }
     }
   }
@@ -1016,7 +1106,42 @@ __global__ __launch_bounds__(256) void k_lora_mid(const float* __restrict__ x, i
   for (int r = 0; r < 4; ++r) xr[r] = x + (size_t)min(r0 + r, m - 1) * k;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const int chunks = k >> 3;
-  for (int c = 0; c < chunks; ++c) {
+  // Groups of 8 chunks, double-buffered: the loads of the next group are in
+  // flight while the current one is added in order.
+  struct Grp {
+    float av[8], xv[4][8];
+  };
+  auto load = [&](Grp& g, int c) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      g.av[u] = arow[8 * (c + u) + i];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) g.xv[r][u] = xr[r][8 * (c + u) + i];
+    }
+  };
+  auto add = [&](const Grp& g) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] = acc[r] + g.xv[r][u] * g.av[u];
+  };
+  int c = 0;
+  if (chunks >= 8) {
+    Grp g0, g1;
+    load(g0, 0);
+    c = 8;
+    while (true) {
+      if (c + 8 > chunks) { add(g0); break; }
+      load(g1, c);
+      c += 8;
+      add(g0);
+      if (c + 8 > chunks) { add(g1); break; }
+      load(g0, c);
+      c += 8;
+      add(g1);
+    }
+  }
+  for (; c < chunks; ++c) {
     const float av = arow[8 * c + i];
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[r] = acc[r] + xr[r][8 * c + i] * av;
