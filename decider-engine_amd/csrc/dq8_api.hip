@@ -12,6 +12,10 @@ struct dq8_ctx {
   // only dq8_linear_f32in and K % 64 != 0 inputs use it.
   void* work = nullptr;
   size_t work_bytes = 0;
+  // Workspace of dq8_ffn (the re-quantized SwiGlu product and the down adapter's
+  // middle product), kept apart from `work`, which the projections it launches use.
+  void* chain = nullptr;
+  size_t chain_bytes = 0;
   uint32_t* flag = nullptr;  // non-finite flag for synchronous checks
 };
 
@@ -46,22 +50,23 @@ dq8_status from_hip(hipError_t e) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-dq8_status ensure_work(dq8_ctx* ctx, size_t bytes) {
-  if (bytes <= ctx->work_bytes) return DQ8_OK;
-  if (ctx->work) {
+dq8_status ensure_buffer(void*& buf, size_t& have, size_t bytes) {
+  if (bytes <= have) return DQ8_OK;
+  if (buf) {
     // Earlier work queued on any stream may still read the old buffer.
     hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) return from_hip(e);
-    (void)hipFree(ctx->work);
-    ctx->work = nullptr;
-    ctx->work_bytes = 0;
+    (void)hipFree(buf);
+    buf = nullptr;
+    have = 0;
   }
   size_t want = bytes + (bytes >> 2);
-  hipError_t e = hipMalloc(&ctx->work, want);
+  hipError_t e = hipMalloc(&buf, want);
   if (e != hipSuccess) return from_hip(e);
-  ctx->work_bytes = want;
+  have = want;
   return DQ8_OK;
 }
+dq8_status ensure_work(dq8_ctx* ctx, size_t bytes) { return ensure_buffer(ctx->work, ctx->work_bytes, bytes); }
 
 dq8_status make_weights(dq8_ctx* ctx, size_t n, size_t k, dq8_weights** out) {
   if (n == 0 || k == 0 || n > (1u << 30) || k > (1u << 30) || n * k > ((size_t)1 << 40)) return DQ8_ERR_SHAPE;
@@ -188,8 +193,19 @@ dq8_status check_item_args(const dq8_weights* w, const int8_t* q, const float* s
   return DQ8_OK;
 }
 
+// Quantized copy of a projection's stored result: q [m][n], scales [m][G].
+struct QOut {
+  int8_t* q;
+  float* scales;
+  uint32_t* nonfinite;
+};
+
 // Split items by kernel kind and launch.  Items with m == 0 do nothing (tensor.rs:152-154).
-dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, int32_t* dots, hipStream_t s) {
+// qout (one item only): the item's stored result is then quantized by k_quantize.
+// (Quantizing in the projection's epilogue was measured slower: the projection
+// kernels are VALU-bound, the quantize pass is memory-bound.)
+dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, int32_t* dots, hipStream_t s,
+                      const QOut* qout = nullptr) {
   size_t need = 0;
   for (size_t i = 0; i < count; ++i) {
     if (!items[i].m) continue;
@@ -251,6 +267,12 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     hipError_t e = dq8::launch_linear(batch[kind], kind, dots != nullptr, s);
     if (e != hipSuccess) return from_hip(e);
   }
+  if (qout && count == 1 && items[0].m > 0) {
+    const dq8::Weights& w = items[0].w->w;
+    hipError_t e = dq8::launch_quantize(items[0].out, (int)items[0].m, w.n, qout->q, w.n, qout->scales,
+                                        (w.n + kGroup - 1) / kGroup, qout->nonfinite, s);
+    if (e != hipSuccess) return from_hip(e);
+  }
   return DQ8_OK;
 }
 
@@ -294,6 +316,7 @@ dq8_status dq8_destroy(dq8_ctx* ctx) {
   DeviceGuard guard(ctx->device);
   (void)hipDeviceSynchronize();
   (void)hipFree(ctx->work);
+  (void)hipFree(ctx->chain);
   (void)hipFree(ctx->flag);
   delete ctx;
   return DQ8_OK;
@@ -474,6 +497,94 @@ dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, 
   const int kind = kind_of(w->w, m);
   place_proj(p, kind, b);
   return from_hip(dq8::launch_linear(b, kind, false, s));
+}
+
+namespace {
+// A result quantization whose non-finite report is synchronous (nonfinite ==
+// NULL): zero the context flag before, read it after.
+dq8_status finish_nonfinite(dq8_ctx* ctx, hipStream_t s) {
+  uint32_t host = 0;
+  hipError_t e = hipMemcpyAsync(&host, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return from_hip(e);
+  return host ? DQ8_ERR_NONFINITE : DQ8_OK;
+}
+}  // namespace
+
+dq8_status dq8_linear_q(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, const float* scales, size_t m,
+                        const float* bias, const dq8_lora* lora, float* out, dq8_epilogue epilogue, int8_t* q_out,
+                        float* scales_out, uint32_t* nonfinite, void* stream) {
+  if (!ctx) return DQ8_ERR_ARG;
+  if (m == 0) return w ? DQ8_OK : DQ8_ERR_ARG;
+  dq8_status st = check_item_args(w, q, scales, m, out, DQ8_ROWS, epilogue);
+  if (st == DQ8_OK) st = check_lora(lora);
+  if (st != DQ8_OK) return st;
+  if (!q_out || !scales_out) return DQ8_ERR_ARG;
+  if (w->w.device != ctx->device) return DQ8_ERR_ARG;
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = (hipStream_t)stream;
+  if (!nonfinite) {
+    hipError_t e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  QOut qo = {q_out, scales_out, nonfinite ? nonfinite : ctx->flag};
+  dq8_linear_item it = {w, q, scales, m, bias, out, DQ8_ROWS, epilogue, lora};
+  st = run_linear(ctx, &it, 1, nullptr, s, &qo);
+  if (st != DQ8_OK || nonfinite) return st;
+  return finish_nonfinite(ctx, s);
+}
+
+dq8_status dq8_ffn(dq8_ctx* ctx, const dq8_ffn_weights* f, const int8_t* q, const float* scales, size_t m, float* h,
+                   float* residual, uint32_t* nonfinite, void* stream) {
+  if (!ctx || !f || !f->gate || !f->up || !f->down) return DQ8_ERR_ARG;
+  if (m == 0) return DQ8_OK;
+  const dq8::Weights &g = f->gate->w, &u = f->up->w, &d = f->down->w;
+  if (g.k != u.k || g.n != u.n || d.k != u.n) return DQ8_ERR_SHAPE;
+  if (!q || !scales || !h || !residual) return DQ8_ERR_ARG;
+  if (g.device != ctx->device || u.device != ctx->device || d.device != ctx->device) return DQ8_ERR_ARG;
+  dq8_status st = check_lora(f->gate_lora);
+  if (st == DQ8_OK) st = check_lora(f->up_lora);
+  if (st != DQ8_OK) return st;
+  const size_t rank = f->down_lora_a ? f->down_lora_rank : 0;
+  if (f->down_lora_a && (!f->down_lora_b || rank == 0 || rank > (1u << 20))) return DQ8_ERR_ARG;
+  if (m > (1u << 30)) return DQ8_ERR_SHAPE;
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = (hipStream_t)stream;
+  // chain workspace: q_h [m][inter], scales_h [m][G] (16-byte aligned), down mid [m][rank]
+  const size_t inter = (size_t)u.n, gh = (inter + kGroup - 1) / kGroup;
+  const size_t qbytes = (m * inter + 255) / 256 * 256, sbytes = (m * gh * sizeof(float) + 255) / 256 * 256;
+  st = ensure_buffer(ctx->chain, ctx->chain_bytes, qbytes + sbytes + m * rank * sizeof(float));
+  if (st != DQ8_OK) return st;
+  int8_t* qh = (int8_t*)ctx->chain;
+  float* sh = (float*)((char*)ctx->chain + qbytes);
+  float* mid = (float*)((char*)ctx->chain + qbytes + sbytes);
+  if (!nonfinite) {
+    hipError_t e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  // gate: Write into h (qwen.rs:489); up: SwiGlu into h, quantized on the fly (qwen.rs:490-491)
+  dq8_linear_item gi = {f->gate, q, scales, m, f->gate_bias, h, DQ8_ROWS, DQ8_WRITE, f->gate_lora};
+  st = run_linear(ctx, &gi, 1, nullptr, s);
+  if (st != DQ8_OK) return st;
+  QOut qo = {qh, sh, nonfinite ? nonfinite : ctx->flag};
+  dq8_linear_item ui = {f->up, q, scales, m, f->up_bias, h, DQ8_ROWS, DQ8_SWIGLU, f->up_lora};
+  st = run_linear(ctx, &ui, 1, nullptr, s, &qo);
+  if (st != DQ8_OK) return st;
+  if (!nonfinite) {
+    // QuantizedInputs::new(h) returned None: the crate's down projection takes its
+    // FP32 path on h (tensor.rs:197-201), which is the caller's to run.
+    st = finish_nonfinite(ctx, s);
+    if (st != DQ8_OK) return st;
+  }
+  // down: Add into the residual (qwen.rs:492), its adapter's middle product from h
+  dq8_lora dl = {mid, f->down_lora_b, rank, f->down_lora_scale};
+  if (rank > 0) {
+    hipError_t e = dq8::launch_lora_mid(h, (int)m, (int)inter, f->down_lora_a, (int)rank, mid, s);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  dq8_linear_item di = {f->down, qh, sh, m, f->down_bias, residual, DQ8_ROWS, DQ8_ADD,
+                        f->down_lora_a ? &dl : nullptr};
+  return run_linear(ctx, &di, 1, nullptr, s);
 }
 
 dq8_status dq8_group_dots(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, size_t m, int32_t* dots,

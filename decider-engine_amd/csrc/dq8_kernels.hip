@@ -54,10 +54,53 @@ __device__ __forceinline__ v32f concat(v16i lo, v16i hi) {
 }
 __device__ __forceinline__ v4i load16(const void* p) { return *reinterpret_cast<const v4i*>(p); }
 
-// silu (decider-engine src/qwen.rs:194-199): x * (1 / (1 + exp(-x))).
-// exp is evaluated in double and rounded once to float.
+// 2^(j/32), j = 0..31, correctly rounded to double.
+__constant__ double kExp2Frac[32] = {
+    0x1.0000000000000p+0, 0x1.059b0d3158574p+0, 0x1.0b5586cf9890fp+0, 0x1.11301d0125b51p+0,
+    0x1.172b83c7d517bp+0, 0x1.1d4873168b9aap+0, 0x1.2387a6e756238p+0, 0x1.29e9df51fdee1p+0,
+    0x1.306fe0a31b715p+0, 0x1.371a7373aa9cbp+0, 0x1.3dea64c123422p+0, 0x1.44e086061892dp+0,
+    0x1.4bfdad5362a27p+0, 0x1.5342b569d4f82p+0, 0x1.5ab07dd485429p+0, 0x1.6247eb03a5585p+0,
+    0x1.6a09e667f3bcdp+0, 0x1.71f75e8ec5f74p+0, 0x1.7a11473eb0187p+0, 0x1.82589994cce13p+0,
+    0x1.8ace5422aa0dbp+0, 0x1.93737b0cdc5e5p+0, 0x1.9c49182a3f090p+0, 0x1.a5503b23e255dp+0,
+    0x1.ae89f995ad3adp+0, 0x1.b7f76f2fb5e47p+0, 0x1.c199bdd85529cp+0, 0x1.cb720dcef9069p+0,
+    0x1.d5818dcfba487p+0, 0x1.dfc97337b9b5fp+0, 0x1.ea4afa2a490dap+0, 0x1.f50765b6e4540p+0};
+
+// expf as the reference's f32::exp computes it: Rust lowers it to the libm
+// expf of the host, glibc 2.35 on x86-64, whose algorithm (sysdeps/ieee754/
+// flt-32/e_expf.c, from ARM's optimized-routines) is restated here in the
+// form glibc's FMA build runs (__expf_fma, selected on every x86-64 with
+// FMA3):
+//   k = round(x * 32/ln2), r = x * 32/ln2 - k (both from one fused
+//   multiply-add of x, so r is exact), exp(x) = 2^(k/32) * p(r) with
+//   p(r) = (c0 r + c1) r^2 + (c2 r + 1) in double, rounded once to float.
+// The rounding to the nearest integer adds and subtracts 1.5 * 2^52; the low
+// bits of that sum are k, giving the table index (k mod 32) and the exponent
+// (k div 32).  Inputs at or above 89 overflow to +inf and inputs at or below
+// -104 round to +0, as in glibc.
+__device__ __forceinline__ float expf_libm(float x) {
+  if (x != x) return x + x;
+  if (x >= 89.0f) return __builtin_inff();
+  if (x <= -104.0f) return 0.0f;
+  constexpr double kInvLn2x32 = 0x1.71547652b82fep+0 * 32, kShift = 0x1.8p+52;
+  constexpr double c0 = 0x1.c6af84b912394p-20, c1 = 0x1.ebfce50fac4f3p-13, c2 = 0x1.62e42ff0c52d6p-6;
+  const double xd = x;
+  double kd = __builtin_fma(kInvLn2x32, xd, kShift);
+  const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+  kd -= kShift;
+  const double r = __builtin_fma(kInvLn2x32, xd, -kd);
+  const uint32_t j = (uint32_t)ki & 31u;
+  const double s = __builtin_bit_cast(double, __builtin_bit_cast(uint64_t, kExp2Frac[j]) + ((ki - j) << 47));
+  const double z = __builtin_fma(c0, r, c1);
+  const double r2 = r * r;
+  double y = __builtin_fma(c2, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  return (float)(y * s);
+}
+
+// silu (decider-engine src/qwen.rs:194-199): x * (1 / (1 + exp(-x))), each
+// operation one fp32 rounding.
 __device__ __forceinline__ float silu(float x) {
-  float e = (float)exp(-(double)x);
+  const float e = expf_libm(-x);
   return x * (1.0f / (1.0f + e));
 }
 

@@ -48,6 +48,23 @@ class _Lora(ctypes.Structure):
     ]
 
 
+class _FfnWeights(ctypes.Structure):
+    _fields_ = [
+        ("gate", ctypes.c_void_p),
+        ("up", ctypes.c_void_p),
+        ("down", ctypes.c_void_p),
+        ("gate_bias", ctypes.c_void_p),
+        ("up_bias", ctypes.c_void_p),
+        ("down_bias", ctypes.c_void_p),
+        ("gate_lora", ctypes.POINTER(_Lora)),
+        ("up_lora", ctypes.POINTER(_Lora)),
+        ("down_lora_a", ctypes.c_void_p),
+        ("down_lora_b", ctypes.c_void_p),
+        ("down_lora_rank", ctypes.c_size_t),
+        ("down_lora_scale", ctypes.c_float),
+    ]
+
+
 class _Item(ctypes.Structure):
     _fields_ = [
         ("w", ctypes.c_void_p),
@@ -94,6 +111,8 @@ def lib() -> ctypes.CDLL:
         "dq8_linear_batch": ([_vp, ctypes.POINTER(_Item), _sz, _vp], _i),
         "dq8_lora_mid": ([_vp, _vp, _sz, _sz, _vp, _sz, _vp, _vp], _i),
         "dq8_linear_lora": ([_vp, _vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
+        "dq8_linear_q": ([_vp, _vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _vp, _vp, _vp, _vp], _i),
+        "dq8_ffn": ([_vp, ctypes.POINTER(_FfnWeights), _vp, _vp, _sz, _vp, _vp, _vp, _vp], _i),
         "dq8_group_dots": ([_vp, _vp, _vp, _sz, _vp, _vp], _i),
         "dq8_status_string": ([_i], ctypes.c_char_p),
     }
@@ -322,6 +341,60 @@ class Context:
                                      ctypes.byref(lo), out.data_ptr(), layout, epilogue, _stream(self.device)),
                "dq8_linear_lora")
         return out
+
+    def linear_q(self, w: Weights, q, scales, out=None, bias=None, lora: Lora | None = None, epilogue=WRITE,
+                 nonfinite=None):
+        """The projection (rows layout) plus QuantizedInputs::new of its stored result:
+        returns (out, q_out, scales_out).  Raises NonFinite like dq8_quantize unless
+        `nonfinite` (a zeroed int32 device scalar) is given."""
+        torch = _torch()
+        self._dev(q, torch.int8, name="q")
+        m, k = q.shape
+        if k != w.k:
+            raise Dq8Error(ERR_SHAPE, "dq8_linear_q: input width differs from the weights")
+        self._dev(scales, torch.float32, (m, groups(k)), "scales")
+        if out is None:
+            out = torch.zeros((m, w.n), dtype=torch.float32, device=self.device)
+        self._dev(out, torch.float32, (m, w.n), "out")
+        if bias is not None:
+            self._dev(bias, torch.float32, (w.n,), "bias")
+        qo = torch.empty((m, w.n), dtype=torch.int8, device=self.device)
+        so = torch.empty((m, groups(w.n)), dtype=torch.float32, device=self.device)
+        lo = None if lora is None else ctypes.byref(self._lora(lora, m, w.n))
+        _check(lib().dq8_linear_q(self.handle, w.handle, q.data_ptr(), scales.data_ptr(), m, _ptr(bias), lo,
+                                  out.data_ptr(), epilogue, qo.data_ptr(), so.data_ptr(), _ptr(nonfinite),
+                                  _stream(self.device)), "dq8_linear_q")
+        return out, qo, so
+
+    def ffn(self, gate: Weights, up: Weights, down: Weights, q, scales, residual, h=None, biases=(None, None, None),
+            gate_lora: Lora | None = None, up_lora: Lora | None = None, down_lora=None, nonfinite=None):
+        """One layer's FFN chain (qwen.rs:486-492): h = silu(gate(x)) * up(x); residual += down(h).
+        down_lora = (lora_A [rank][inter], lora_B [hidden][rank], scale) or None.  Returns h."""
+        torch = _torch()
+        self._dev(q, torch.int8, name="q")
+        m, k = q.shape
+        self._dev(scales, torch.float32, (m, groups(k)), "scales")
+        if h is None:
+            h = torch.zeros((m, up.n), dtype=torch.float32, device=self.device)
+        self._dev(h, torch.float32, (m, up.n), "h")
+        self._dev(residual, torch.float32, (m, down.n), "residual")
+        fw = _FfnWeights(gate.handle, up.handle, down.handle, *[_ptr(b) for b in biases])
+        keep = []
+        if gate_lora is not None:
+            keep.append(self._lora(gate_lora, m, gate.n))
+            fw.gate_lora = ctypes.pointer(keep[-1])
+        if up_lora is not None:
+            keep.append(self._lora(up_lora, m, up.n))
+            fw.up_lora = ctypes.pointer(keep[-1])
+        if down_lora is not None:
+            a, b, sc = down_lora
+            self._dev(a, torch.float32, (a.shape[0], up.n), "down lora_A")
+            self._dev(b, torch.float32, (down.n, a.shape[0]), "down lora_B")
+            fw.down_lora_a, fw.down_lora_b, fw.down_lora_rank, fw.down_lora_scale = a.data_ptr(), b.data_ptr(), \
+                a.shape[0], sc
+        _check(lib().dq8_ffn(self.handle, ctypes.byref(fw), q.data_ptr(), scales.data_ptr(), m, h.data_ptr(),
+                             residual.data_ptr(), _ptr(nonfinite), _stream(self.device)), "dq8_ffn")
+        return h
 
     def linear_f32in(self, w: Weights, x, out=None, bias=None, layout=ROWS, epilogue=WRITE):
         torch = _torch()

@@ -132,6 +132,43 @@ dq8_status dq8_lora_mid(dq8_ctx *ctx, const float *x, size_t m, size_t k, const 
 dq8_status dq8_linear_lora(dq8_ctx *ctx, const dq8_weights *w, const int8_t *q, const float *scales, size_t m,
                            const float *bias, const dq8_lora *lora, float *out, dq8_layout layout,
                            dq8_epilogue epilogue, void *stream);
+/* dq8_linear_lora (lora may be NULL) in the rows layout whose stored result
+ * out [m][n] is also quantized per token, as QuantizedInputs::new quantizes the
+ * next projection's input (tensor.rs:315-353): q_out int8 [m][n] and scales_out
+ * [m][ceil(n/64)].  This is the FFN's re-quantization of the SwiGlu product
+ * before the down projection (qwen.rs:490-492).  A non-finite value in out is
+ * reported as by dq8_quantize:
+ * nonfinite == NULL synchronizes and returns DQ8_ERR_NONFINITE (q_out/scales_out
+ * then unspecified; out is written); otherwise 1 is ORed into *nonfinite. */
+dq8_status dq8_linear_q(dq8_ctx *ctx, const dq8_weights *w, const int8_t *q, const float *scales, size_t m,
+                        const float *bias, const dq8_lora *lora, float *out, dq8_epilogue epilogue, int8_t *q_out,
+                        float *scales_out, uint32_t *nonfinite, void *stream);
+/* The weights of one layer's SwiGLU FFN (qwen.rs:486-492) and their optional
+ * adapters.  gate/up adapters come with their middle products (dq8_lora_mid of
+ * the FFN input x); the down adapter's middle product is computed from the
+ * SwiGlu product h inside dq8_ffn, so its lora_A [rank][inter] is given instead. */
+typedef struct dq8_ffn_weights {
+    const dq8_weights *gate, *up, *down;  /* [inter][hidden], [inter][hidden], [hidden][inter] */
+    const float *gate_bias, *up_bias, *down_bias;  /* NULL: +0.0 */
+    const dq8_lora *gate_lora, *up_lora;           /* NULL: none */
+    const float *down_lora_a, *down_lora_b;        /* NULL: none; [rank][inter], [hidden][rank] */
+    size_t down_lora_rank;
+    float down_lora_scale;
+} dq8_ffn_weights;
+/* One layer's FFN chain on the device (qwen.rs:486-492):
+ *   h = gate(x)                          Write            (Linear::apply_shared)
+ *   h = silu(h) * up(x)                  SwiGlu           (apply_into_shared)
+ *   residual += down(h)                  Add, h re-quantized per token (apply_into)
+ * q/scales are the FFN input's quantization, shared by gate and up (the
+ * SharedInput of qwen.rs:488).  h [m][inter] is written (the crate's `gate`
+ * buffer) and quantized on the device for down.  If h holds a
+ * non-finite value the crate's down projection takes its FP32 path: with
+ * nonfinite == NULL this call synchronizes after up and returns
+ * DQ8_ERR_NONFINITE with h written and residual untouched, for the caller's FP32
+ * path; otherwise it ORs 1 into *nonfinite and runs down anyway (its result then
+ * to be discarded by the caller). */
+dq8_status dq8_ffn(dq8_ctx *ctx, const dq8_ffn_weights *f, const int8_t *q, const float *scales, size_t m, float *h,
+                   float *residual, uint32_t *nonfinite, void *stream);
 /* Several independent projections in one launch (same-shape inputs are not
  * required).  Each item is one dq8_linear (or dq8_linear_lora).  This is the shape of a model
  * layer's projections that read already-available inputs (q/k/v, GDN

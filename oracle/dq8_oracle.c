@@ -198,6 +198,84 @@ void dq8o_linear_int8(const int8_t *q, const float *xs, size_t rows, const uint8
  * f32::exp lowers to the platform libm expf. */
 float dq8o_silu(float x) { return x * (1.0f / (1.0f + expf(-x))); }
 
+struct sctx { const float *x; float *y; };
+static void silu_range(void *c, size_t b, size_t e) {
+    struct sctx *s = (struct sctx *)c;
+    for (size_t i = b; i < e; ++i) s->y[i] = dq8o_silu(s->x[i]);
+}
+/* dq8o_silu over an array. */
+void dq8o_silu_n(const float *x, float *y, size_t n, int threads) {
+    struct sctx c = {x, y};
+    parallel_for(n, n >= (1u << 16) ? threads : 1, silu_range, &c);
+}
+
+/* The algorithm of the libm expf that f32::exp lowers to on the reference's
+ * platform: glibc 2.35 on x86-64 (sysdeps/ieee754/flt-32/e_expf.c, from ARM's
+ * optimized-routines), in the form of glibc's FMA build (__expf_fma, chosen on
+ * every x86-64 with FMA3).  With n = 32 and InvLn2N = n / ln 2:
+ *   kd = fma(InvLn2N, x, 1.5*2^52)  -> low bits of kd hold k = round(x n/ln2)
+ *   r  = fma(InvLn2N, x, -(kd - 1.5*2^52))
+ *   s  = 2^(k/n) from a table of 2^(j/n), j = k mod n, and the exponent k div n
+ *   y  = fma(fma(c0, r, c1), r*r, fma(c2, r, 1)) * s, rounded once to float,
+ * with c0..c2 the cubic's coefficients for 2^(r/n).  x >= 89 overflows to
+ * +inf, x <= -104 gives +0, NaN returns x + x.  The kernels restate the same
+ * steps; dq8o_silu itself calls libm expf.  Pinned against the host expf on
+ * every binary32 input (dq8o_expf_mismatches). */
+static uint64_t exp2_frac_bits[32];
+static pthread_once_t exp2_frac_once = PTHREAD_ONCE_INIT;
+static void exp2_frac_init(void) {
+    for (int j = 0; j < 32; ++j) {
+        double v = exp2((double)j / 32.0);
+        memcpy(&exp2_frac_bits[j], &v, 8);
+    }
+}
+float dq8o_expf_restated(float x) {
+    if (x != x) return x + x;
+    if (x >= 89.0f) return INFINITY;
+    if (x <= -104.0f) return 0.0f;
+    pthread_once(&exp2_frac_once, exp2_frac_init);
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    double xd = (double)x;
+    double kd = fma(inv_ln2_n, xd, shift);
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    double r = fma(inv_ln2_n, xd, -kd);
+    uint64_t j = ki & 31u, sb = exp2_frac_bits[j] + ((ki - j) << 47);
+    double s;
+    memcpy(&s, &sb, 8);
+    double z = fma(c0, r, c1), r2 = r * r, y = fma(c2, r, 1.0);
+    y = fma(z, r2, y);
+    return (float)(y * s);
+}
+
+struct ectx { uint64_t base; size_t mismatches; };
+static void expf_range(void *c, size_t b, size_t e) {
+    struct ectx *x = (struct ectx *)c;
+    size_t bad = 0;
+    for (size_t i = b; i < e; ++i) {
+        uint32_t bits = (uint32_t)(x->base + i);
+        float v, want, got;
+        memcpy(&v, &bits, 4);
+        want = expf(v);
+        got = dq8o_expf_restated(v);
+        bad += memcmp(&want, &got, 4) != 0;
+    }
+    __atomic_fetch_add(&x->mismatches, bad, __ATOMIC_RELAXED);
+}
+/* Number of binary32 bit patterns in [begin, end) (end <= 2^32) where
+ * dq8o_expf_restated differs in any bit from the host libm expf. */
+size_t dq8o_expf_mismatches(uint64_t begin, uint64_t end, int threads) {
+    if (end > (1ull << 32)) end = 1ull << 32;
+    if (end <= begin) return 0;
+    struct ectx c = {begin, 0};
+    pthread_once(&exp2_frac_once, exp2_frac_init);
+    parallel_for((size_t)(end - begin), threads, expf_range, &c);
+    return c.mismatches;
+}
+
 /* write_columns (tensor.rs:272-288) with Epilogue::store (tensor.rs:92-99):
  * 0 Write (dst = v), 1 Add (dst += v), 2 SwiGlu (dst = silu(dst) * v). */
 void dq8o_write_columns(const float *columns, size_t rows, size_t outputs, float *result, int epilogue) {

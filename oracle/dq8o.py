@@ -43,6 +43,12 @@ def lib():
         L.dq8o_linear_int8.restype = None
         L.dq8o_silu.argtypes = [ctypes.c_float]
         L.dq8o_silu.restype = ctypes.c_float
+        L.dq8o_silu_n.argtypes = [_f32p, _f32p, _sz, ctypes.c_int]
+        L.dq8o_silu_n.restype = None
+        L.dq8o_expf_restated.argtypes = [ctypes.c_float]
+        L.dq8o_expf_restated.restype = ctypes.c_float
+        L.dq8o_expf_mismatches.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int]
+        L.dq8o_expf_mismatches.restype = ctypes.c_size_t
         L.dq8o_write_columns.argtypes = [_f32p, _sz, _sz, _f32p, ctypes.c_int]
         L.dq8o_write_columns.restype = None
         L.dq8o_linear.argtypes = [_f32p, _sz, _sz, _u8p, _f32p, _sz, ctypes.c_void_p, _f32p, ctypes.c_int, ctypes.c_int]
@@ -145,6 +151,24 @@ def write_columns(columns: np.ndarray, result: np.ndarray, epilogue: int) -> np.
 
 def silu(x: float) -> np.float32:
     return np.float32(lib().dq8o_silu(float(x)))
+
+
+def silu_n(x: np.ndarray, threads: int = 1) -> np.ndarray:
+    """dq8o_silu elementwise over a float32 array (any shape)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().dq8o_silu_n(x, y, x.size, threads)
+    return y
+
+
+def expf_restated(x: float) -> np.float32:
+    """The restated glibc expf algorithm (the one the kernels run)."""
+    return np.float32(lib().dq8o_expf_restated(float(x)))
+
+
+def expf_mismatches(begin: int, end: int, threads: int = 1) -> int:
+    """Bit patterns in [begin, end) where the restated expf differs from libm's."""
+    return int(lib().dq8o_expf_mismatches(begin, end, threads))
 
 
 def linear(x, w, ws, bias=None, result=None, epilogue: int = 0, threads: int = 1):

@@ -499,3 +499,100 @@ def test_planted_dot_scores_faults_are_detected():
     e = 1 + 2.0 ** -12
     fused = f32(e * e - (1 + 2.0 ** -11))  # what an FMA would leave in lane 0
     assert fused != 0.0
+
+
+# ---------------------------------------------------------------- silu / expf
+# qwen.rs:194-199 computes silu with f32::exp, i.e. the host libm expf (glibc
+# 2.35 on x86-64).  The kernels restate glibc's algorithm; these tests pin the
+# restatement (dq8o_expf_restated, the same steps as the kernels) to libm.
+
+def _libm_expf():
+    import ctypes
+    import ctypes.util
+    m = ctypes.CDLL(ctypes.util.find_library("m"))
+    m.expf.argtypes = [ctypes.c_float]
+    m.expf.restype = ctypes.c_float
+    return m.expf
+
+
+def _exp2_frac_table():
+    """2^(j/32), j = 0..31, from 50-digit decimal arithmetic rounded to double."""
+    from decimal import Decimal, localcontext
+    with localcontext() as c:
+        c.prec = 50
+        return [float(Decimal(2) ** (Decimal(j) / Decimal(32))) for j in range(32)]
+
+
+_EXP2_FRAC = _exp2_frac_table()
+
+
+def _py_expf_unfused(x):
+    """glibc's expf steps in plain double arithmetic, without its fused
+    multiply-adds (the x86-64 build without FMA3)."""
+    tab = _EXP2_FRAC
+    inv = float.fromhex("0x1.71547652b82fep+0") * 32
+    shift = float.fromhex("0x1.8p+52")
+    c0 = float.fromhex("0x1.c6af84b912394p-5") / 32 ** 3
+    c1 = float.fromhex("0x1.ebfce50fac4f3p-3") / 32 ** 2
+    c2 = float.fromhex("0x1.62e42ff0c52d6p-1") / 32
+    z = inv * x
+    kd = z + shift
+    ki = struct.unpack("<Q", struct.pack("<d", kd))[0]
+    kd -= shift
+    r = z - kd
+    j = ki & 31
+    sb = (struct.unpack("<Q", struct.pack("<d", tab[j]))[0] + ((ki - j) << 47)) % (1 << 64)
+    s = struct.unpack("<d", struct.pack("<Q", sb))[0]
+    y = (c0 * r + c1) * (r * r) + (c2 * r + 1.0)
+    return f32(y * s)
+
+
+def test_restated_expf_matches_libm_on_every_binary32_input():
+    assert dq8o.expf_mismatches(0, 1 << 32, threads=8) == 0
+
+
+def test_expf_known_answers_and_special_values():
+    expf = _libm_expf()
+    assert dq8o.expf_restated(0.0) == 1.0 and dq8o.expf_restated(-0.0) == 1.0
+    assert dq8o.expf_restated(1.0) == F32(float.fromhex("0x1.5bf0a8p+1"))  # e to nearest
+    assert dq8o.expf_restated(float("inf")) == np.inf and dq8o.expf_restated(-np.inf) == 0.0
+    assert np.isnan(dq8o.expf_restated(float("nan")))
+    assert dq8o.expf_restated(89.0) == np.inf and dq8o.expf_restated(-104.0) == 0.0
+    # smallest subnormal region and the largest finite result
+    for h in ("-0x1.9fe368p+6", "-0x1.9fe36ap+6", "0x1.62e42ep+6", "0x1.62e430p+6"):
+        x = f32(float.fromhex(h))
+        assert dq8o.expf_restated(x).tobytes() == F32(expf(x)).tobytes()
+
+
+def test_unfused_expf_agrees_on_ordinary_inputs_but_not_on_glibc_fma_cases():
+    # The plain-double form of the same algorithm agrees with libm on random
+    # inputs (the constants and table are right) but not where glibc's fused
+    # multiply-adds decide the rounding: the restatement must be the fused one.
+    expf = _libm_expf()
+    rng = np.random.default_rng(3)
+    for x in rng.uniform(-80, 80, 2000).astype(np.float32):
+        assert _py_expf_unfused(float(x)) == F32(expf(float(x)))
+    for h in ("0x1.04845ep+5", "-0x1.f8cbb2p+5"):
+        x = f32(float.fromhex(h))
+        assert _py_expf_unfused(x) != F32(expf(x))
+        assert dq8o.expf_restated(x) == F32(expf(x))
+
+
+def test_double_exp_rounded_once_is_not_libm_expf():
+    # A correctly rounded exp differs from glibc's expf (on 170648 of the
+    # 2239889408 inputs in (-104, 89)); one of them:
+    import math
+    expf = _libm_expf()
+    x = f32(float.fromhex("0x1.fefe02p-16"))
+    assert F32(math.exp(x)) != F32(expf(x))
+    assert dq8o.expf_restated(x) == F32(expf(x))
+
+
+def test_silu_n_matches_scalar_silu():
+    rng = np.random.default_rng(9)
+    x = np.concatenate([rng.standard_normal(70000).astype(np.float32) * 20,
+                        np.array([0.0, -0.0, np.inf, -np.inf, 1e-45, -1e-45, 200.0, -200.0], np.float32)])
+    y = dq8o.silu_n(x, threads=4)
+    want = np.array([dq8o.silu(float(v)) for v in x], np.float32)
+    assert y.tobytes() == want.tobytes()
+    assert dq8o.silu(0.0) == 0.0 and dq8o.silu(-200.0) == 0.0 and dq8o.silu(200.0) == 200.0
