@@ -15,7 +15,8 @@ activations Student-t(3), seeded; all inputs are resident in HBM.
 Secondary workload (reported under "skinny"): 16 questions x 24 tokens, each
 question one grouped skinny launch over one layer's projection set (q, k, v, o,
 GDN in/out, FFN gate/up/down), rotating 5 weight copies (> 256 MB MALL) so
-weight bytes come from HBM.
+weight bytes come from HBM.  "questions_stacked" runs the same questions layer
+by layer with their rows stacked into one 384-row launch per layer set.
 
 "roofline" is for the dominant kernel (the wide projection kernel): achieved
 = algorithmic int8 ops per launch / its average launch time from HIP events on
@@ -265,7 +266,7 @@ def main():
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
 
-    skinny = run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen)
+    stacked, skinny = run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen)
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, torch, dq8, ctx, dev, gen)
     traffic = load_traffic("linear_wide_stack2048")
     out = {
@@ -304,6 +305,7 @@ def main():
             "avg_launch_ms": round(lin_avg_ms, 5),
         },
         "skinny": skinny,
+        "questions_stacked": stacked,
         "lora": lora,
         "cpu_baseline": cpu,
     }
@@ -406,10 +408,12 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
     warm_ms = t0.elapsed_time(t1)
     gbs = wbytes * args.questions * reps / (total_ms * 1e-3) / 1e9
     kernel_gbs = wbytes / (avg_launch * 1e-3) / 1e9
+    stacked = run_stacked(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, wbytes,
+                          total_ms / (reps * args.questions))
     for ws in copies:
         for h in ws:
             h.free()
-    return {
+    return stacked, {
         "workload": f"{args.questions} questions x {M} tokens, one grouped launch per question over q,k,v,o,"
                     f"GDN in/out, FFN gate/up/down ({args.weight_copies} rotating weight copies)",
         "value": round(gbs, 1),
@@ -428,6 +432,54 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
             "bytes_per_launch": wbytes,
             "avg_launch_ms": round(avg_launch, 5),
         },
+    }
+
+
+def run_stacked(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, wbytes, per_question_ms):
+    """The same questions continued layer by layer: every question's token rows
+    stacked into one projection launch per layer set (M = questions x tokens),
+    so a layer's weights are read once for all questions.  Weight copies rotate
+    per launch as in the per-question schedule."""
+    M = args.questions * args.question_tokens
+    sets = []
+    keep = []
+    for ws in copies:
+        items = (dq8._Item * len(shapes))()
+        for j, (_, n, k) in enumerate(shapes):
+            q, s = ctx.quantize(torch.randn((M, k), generator=gen, device=dev))
+            o = torch.empty((M, n), dtype=torch.float32, device=dev)
+            keep += [q, s, o]
+            items[j] = dq8._Item(ws[j].handle, q.data_ptr(), s.data_ptr(), M, None, o.data_ptr(), dq8.ROWS,
+                                 dq8.WRITE)
+        sets.append(items)
+    sh = stream.cuda_stream
+
+    def go(i):
+        st = lib.dq8_linear_batch(ctx.handle, sets[i % len(sets)], len(shapes), sh)
+        if st != 0:
+            raise dq8.Dq8Error(st, "dq8_linear_batch")
+
+    for i in range(len(sets)):
+        go(i)
+    torch.cuda.synchronize()
+    reps = 10 * len(sets)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(reps):
+        go(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / reps
+    ops = sum(2 * M * n * k for _, n, k in shapes)
+    del keep
+    return {
+        "workload": f"{args.questions} questions x {args.question_tokens} tokens stacked into one {M}-row launch per "
+                    f"layer set (q,k,v,o, GDN in/out, FFN gate/up/down; {len(copies)} rotating weight copies)",
+        "ms_per_layer_set": round(ms, 5),
+        "ms_per_question": round(ms / args.questions, 5),
+        "tops": round(ops / (ms * 1e-3) / 1e12, 1),
+        "weight_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
+        "speedup_vs_per_question_launches": round(per_question_ms / (ms / args.questions), 2),
     }
 
 

@@ -2,6 +2,7 @@
 #include "../../include/dq8.h"
 #include "dq8_internal.h"
 
+#include <algorithm>
 #include <new>
 #include <stdint.h>
 #include <string.h>
@@ -228,15 +229,6 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     if (it.m == 0) continue;
     const dq8::Weights& w = it.w->w;
     if ((w.g > 32) != (pass == 0)) continue;
-    const int kind = kind_of(w, it.m);
-    dq8::Batch& b = batch[kind];
-    if (b.count == dq8::kMaxBatch) {
-      hipError_t e = dq8::launch_linear(b, kind, dots != nullptr, s);
-      if (e != hipSuccess) return from_hip(e);
-      b.count = 0;
-      b.total_waves = 0;
-      b.any_lora = 0;
-    }
     const int8_t* q = it.q;
     int ldq = w.k;
     if (needs_pad(w, it.q)) {
@@ -257,10 +249,36 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
       xs = dst;
       offset += xs_pad_bytes(w, it.m);
     }
-    dq8::Proj& p = b.p[b.count++];
-    fill_proj(p, w, q, ldq, xs, ldxs, it.m, it.bias, it.out, dots, it.layout, it.epilogue, dots ? nullptr : it.lora);
-    if (p.lora) b.any_lora = 1;
-    place_proj(p, kind, b);
+    // 33-64 rows in the rows layout run as two row chunks of at most 32 on the
+    // skinny kernel: the weights are read twice (the chunks run side by side,
+    // so mostly once from HBM), which beats a wide launch of half-empty row
+    // tiles whose long-K blocks trail (measured 44 against 52 us for 48 rows of
+    // a layer's projection set).  Rows are independent, so the results are the
+    // same bits.
+    const bool split = kind_of(w, it.m) == 0 && it.m <= 64 && it.layout == DQ8_ROWS;
+    const int kind = split ? 2 : kind_of(w, it.m);
+    const size_t half = split ? (it.m + 1) / 2 : it.m;
+    for (size_t r0 = 0; r0 < it.m; r0 += half) {
+      const size_t rows = std::min(half, it.m - r0);
+      dq8::Batch& b = batch[kind];
+      if (b.count == dq8::kMaxBatch) {
+        hipError_t e = dq8::launch_linear(b, kind, dots != nullptr, s);
+        if (e != hipSuccess) return from_hip(e);
+        b.count = 0;
+        b.total_waves = 0;
+        b.any_lora = 0;
+      }
+      dq8::Proj& p = b.p[b.count++];
+      // (the dots kernels read neither x scales nor out, which may be stand-ins)
+      fill_proj(p, w, q + r0 * ldq, ldq, dots ? xs : xs + r0 * ldxs, ldxs, rows, it.bias,
+                dots ? it.out : it.out + r0 * w.n, dots ? dots + r0 * w.n * w.g : nullptr, it.layout, it.epilogue,
+                dots ? nullptr : it.lora);
+      if (p.lora) {
+        p.lmid += r0 * p.rank;
+        b.any_lora = 1;
+      }
+      place_proj(p, kind, b);
+    }
   }
   for (int kind = 0; kind < dq8::kKinds; ++kind) {
     if (batch[kind].count == 0) continue;

@@ -396,6 +396,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 #ifndef DQ8_WIDE_WPE
 #define DQ8_WIDE_WPE 0
 #endif
+// Launches of at most this many blocks (three times as many when they mix
+// long and short K) use a ring of STAGES + 1 groups.
+#ifndef DQ8_WIDE_DEEP_BLOCKS
+#define DQ8_WIDE_DEEP_BLOCKS 511
+#endif
 
 // ---------------------------------------------------------------------------
 // Wide projection kernel (M > 32), LDS-staged.  A block of WM x WN waves owns
@@ -1283,14 +1288,25 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
   if (b.total_waves == 0) return hipSuccess;
   const bool lora = !dots && b.any_lora;
   if (kind == 0) {
-    // total_waves counts blocks for the wide kernel
+    // total_waves counts blocks for the wide kernel.  Blocks that run alone on
+    // a CU wait on load latency between groups; a ring one group deeper hides
+    // it.  That is the case for launches of fewer than two blocks per CU, and
+    // for the trailing long-K blocks of a launch that mixes long and short K
+    // (a layer's projection set over a few questions' rows: 22-28% faster for
+    // 96-192 rows, 1-3% at 384).  Elsewhere the deeper ring's LDS costs
+    // occupancy (1% on a 2048-row prefill).
     constexpr int threads = 64 * DQ8_WIDE_WM * DQ8_WIDE_WN;
-#define DQ8_WIDE(D, L)                                                                                     \
-  k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, DQ8_WIDE_STAGES, DQ8_WIDE_XCH, DQ8_WIDE_SWZ, \
-                D, L><<<b.total_waves, threads, 0, s>>>(b)
-    if (dots) DQ8_WIDE(true, false);
-    else if (lora) DQ8_WIDE(false, true);
-    else DQ8_WIDE(false, false);
+    bool has_long = false, has_short = false;
+    for (int i = 0; i < b.count; ++i) (b.p[i].g > 32 ? has_long : has_short) = true;
+    const bool deep = b.total_waves <= DQ8_WIDE_DEEP_BLOCKS ||
+                      (has_long && has_short && b.total_waves <= 3 * DQ8_WIDE_DEEP_BLOCKS);
+#define DQ8_WIDE(S, D, L)                                                                               \
+  k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, S, DQ8_WIDE_XCH, DQ8_WIDE_SWZ, D, L> \
+      <<<b.total_waves, threads, 0, s>>>(b)
+    constexpr int S0 = DQ8_WIDE_STAGES, S1 = DQ8_WIDE_STAGES + 1;
+    if (dots) DQ8_WIDE(S0, true, false);
+    else if (lora) deep ? DQ8_WIDE(S1, false, true) : DQ8_WIDE(S0, false, true);
+    else deep ? DQ8_WIDE(S1, false, false) : DQ8_WIDE(S0, false, false);
 #undef DQ8_WIDE
     return hipGetLastError();
   }

@@ -117,7 +117,7 @@ def test_weights_from_quantized_round_trip(ctx, n, k):
 # -------------------------------------------------------------- group dots
 
 DOT_SHAPES = [(1, 64, 1), (5, 100, 9), (24, 2048, 33), (32, 131, 70), (33, 64, 31), (67, 192, 65), (130, 257, 40),
-              (24, 6144, 20), (17, 2371, 33), (9, 4160, 18)]
+              (24, 6144, 20), (17, 2371, 33), (9, 4160, 18), (48, 2048, 40), (61, 4160, 17)]
 
 
 @pytest.mark.parametrize("m,k,n", DOT_SHAPES)
@@ -148,7 +148,8 @@ def test_group_dots_extremes(ctx):
 # step, several x-scale chunks, K % 64 != 0).
 LINEAR_SHAPES = [(1, 1, 1), (1, 64, 4), (4, 64, 4), (5, 128, 6), (9, 192, 31), (24, 2048, 100), (32, 131, 70),
                  (33, 100, 9), (67, 128, 8), (64, 2048, 64), (128, 2048, 130), (200, 65, 17), (7, 6144, 33),
-                 (24, 6144, 70), (17, 2371, 50), (32, 4096, 40), (16, 2112, 33), (2, 2113, 17)]
+                 (24, 6144, 70), (17, 2371, 50), (32, 4096, 40), (16, 2112, 33), (2, 2113, 17), (48, 2048, 96),
+                 (40, 6144, 50), (63, 131, 33), (34, 4160, 20), (96, 2048, 64)]
 
 
 @pytest.mark.parametrize("m,k,n", LINEAR_SHAPES)
@@ -166,7 +167,7 @@ def test_linear_rows_write_bit_exact(ctx, m, k, n, with_bias):
     assert bits_equal(host(out), want)
 
 
-@pytest.mark.parametrize("m,k,n", [(5, 128, 6), (24, 2048, 100), (67, 128, 8), (130, 257, 40)])
+@pytest.mark.parametrize("m,k,n", [(5, 128, 6), (24, 2048, 100), (67, 128, 8), (130, 257, 40), (48, 2048, 40)])
 def test_linear_columns_layout_bit_exact(ctx, m, k, n):
     rng = np.random.default_rng(m + k + n)
     x = make_x(rng, m, k)
@@ -179,7 +180,7 @@ def test_linear_columns_layout_bit_exact(ctx, m, k, n):
     assert bits_equal(host(cols), dq8o.linear_int8(qh, sh, wv, ws, threads=4))
 
 
-@pytest.mark.parametrize("m,k,n", [(3, 131, 31), (24, 2048, 64), (67, 192, 65)])
+@pytest.mark.parametrize("m,k,n", [(3, 131, 31), (24, 2048, 64), (67, 192, 65), (45, 6144, 40)])
 def test_linear_add_epilogue_bit_exact(ctx, m, k, n):
     rng = np.random.default_rng(3 * m + k + n)
     x = make_x(rng, m, k)
@@ -193,7 +194,7 @@ def test_linear_add_epilogue_bit_exact(ctx, m, k, n):
     assert bits_equal(host(out), dq8o.linear(x, wv, ws, result=prev, epilogue=1, threads=4))
 
 
-@pytest.mark.parametrize("m,k,n", [(3, 131, 31), (24, 2048, 64), (67, 192, 65)])
+@pytest.mark.parametrize("m,k,n", [(3, 131, 31), (24, 2048, 64), (67, 192, 65), (50, 2048, 70)])
 def test_linear_swiglu_epilogue(ctx, m, k, n):
     rng = np.random.default_rng(5 * m + k + n)
     x = make_x(rng, m, k)
@@ -311,6 +312,79 @@ def test_linear_batch_question_layer_set(ctx):
         assert bits_equal(host(it.out), want)
 
 
+@pytest.mark.parametrize("tokens", [[24, 24], [24, 24, 24, 24], [24, 17, 31, 9, 24, 5, 30, 24], [24] * 16, [40]])
+def test_questions_stacked_rows_match_per_question_launches(ctx, tokens):
+    # Continuation of several questions (lib.rs:512-528 runs them one after
+    # another): stacking their token rows into one projection launch must give
+    # each question the bits of its own launch, since every row is computed on
+    # its own.  A scaled-down layer set with long K, all three epilogues and a
+    # LoRA adapter; the stacked result is also checked against the oracle.
+    rng = np.random.default_rng(sum(tokens) + len(tokens))
+    total = sum(tokens)
+    starts = np.cumsum([0] + tokens)
+    layer = [(2048, 96, dq8.WRITE, False), (6144, 64, dq8.ADD, False), (2048, 160, dq8.SWIGLU, False),
+             (256, 40, dq8.WRITE, True)]
+    stacked, per_q, wants = [], [[] for _ in tokens], []
+    for (k, n, ep, lora) in layer:
+        x = make_x(rng, total, k)
+        wv, ws = dq8o.quantize_weights(make_w(rng, n, k))
+        h = ctx.weights_from_quantized(dev(wv), dev(ws))
+        bias = rng.standard_normal(n).astype(np.float32)
+        base = (rng.standard_normal((total, n)) * 2).astype(np.float32)
+        a = b = None
+        if lora:
+            a = (rng.standard_normal((8, k)) * 0.05).astype(np.float32)
+            b = (rng.standard_normal((n, 8)) * 0.05).astype(np.float32)
+        q, s = ctx.quantize(dev(x))
+        out = dev(base.copy())
+        ad = dq8.Lora(ctx.lora_mid(dev(x), dev(a)), dev(b), 0.5) if lora else None
+        stacked.append(dq8.Item(h, q, s, out, bias=dev(bias), epilogue=ep, lora=ad))
+        if lora:
+            wants.append(dq8o.linear_lora(x, wv, ws, a, b, 0.5, bias=bias, result=base, epilogue=ep, threads=4))
+        else:
+            wants.append(dq8o.linear(x, wv, ws, bias=bias, result=base, epilogue=ep, threads=4))
+        for i in range(len(tokens)):
+            r0, r1 = starts[i], starts[i + 1]
+            qi, si = ctx.quantize(dev(x[r0:r1]))
+            oi = dev(base[r0:r1].copy())
+            adi = dq8.Lora(ctx.lora_mid(dev(x[r0:r1]), dev(a)), dev(b), 0.5) if lora else None
+            per_q[i].append(dq8.Item(h, qi, si, oi, bias=dev(bias), epilogue=ep, lora=adi))
+    ctx.linear_batch(stacked)
+    for items in per_q:
+        ctx.linear_batch(items)
+    for j, want in enumerate(wants):
+        got = host(stacked[j].out)
+        assert bits_equal(got, want)
+        for i in range(len(tokens)):
+            assert bits_equal(host(per_q[i][j].out), got[starts[i]:starts[i + 1]])
+
+
+@pytest.mark.parametrize("ep,lora", [(dq8.WRITE, False), (dq8.SWIGLU, False), (dq8.ADD, True)])
+def test_linear_large_grid_bit_exact(ctx, ep, lora):
+    # 2048 rows x 4096 outputs: 1024 blocks of the wide kernel with uniform K,
+    # the launch shape that keeps the two-group ring (small launches and
+    # mixed-K launches take the three-group ring, covered above).
+    rng = np.random.default_rng(4096 + ep)
+    m, k, n = 2048, 256, 4096
+    x = make_x(rng, m, k)
+    wv, ws = dq8o.quantize_weights(make_w(rng, n, k))
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    bias = rng.standard_normal(n).astype(np.float32)
+    base = (rng.standard_normal((m, n)) * 2).astype(np.float32)
+    q, s = ctx.quantize(dev(x))
+    out = dev(base.copy())
+    if lora:
+        a = (rng.standard_normal((8, k)) * 0.05).astype(np.float32)
+        b = (rng.standard_normal((n, 8)) * 0.05).astype(np.float32)
+        ctx.linear_lora(h, q, s, dq8.Lora(ctx.lora_mid(dev(x), dev(a)), dev(b), 0.5), out=out, bias=dev(bias),
+                        epilogue=ep)
+        want = dq8o.linear_lora(x, wv, ws, a, b, 0.5, bias=bias, result=base, epilogue=ep, threads=8)
+    else:
+        ctx.linear(h, q, s, out=out, bias=dev(bias), epilogue=ep)
+        want = dq8o.linear(x, wv, ws, bias=bias, result=base, epilogue=ep, threads=8)
+    assert bits_equal(host(out), want)
+
+
 def test_config1_single_linear_seed0_bit_exact(ctx):
     # M=128 tokens, K=2048, N=2048; weights N(0, 0.02^2), activations N(0, 1); seed 0
     rng = np.random.default_rng(0)
@@ -346,7 +420,8 @@ def test_lora_mid_bit_exact(ctx, m, k, rank):
 # (m, k, n, rank): skinny (m <= 32, short and long K) and wide kernels; ranks
 # with full chunks of 8, tails, both, and rank 0.
 LORA_SHAPES = [(1, 64, 4, 3), (5, 131, 31, 13), (24, 2048, 96, 16), (17, 6144, 40, 8), (32, 256, 70, 1),
-               (67, 131, 31, 13), (130, 2048, 100, 16), (64, 192, 65, 24), (19, 128, 9, 0)]
+               (67, 131, 31, 13), (130, 2048, 100, 16), (64, 192, 65, 24), (19, 128, 9, 0), (48, 2048, 96, 16),
+               (37, 6144, 40, 8)]
 
 
 def _lora_case(rng, m, k, n, rank):
