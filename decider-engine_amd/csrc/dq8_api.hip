@@ -1,6 +1,7 @@
 // C ABI of include/dq8.h on top of the HIP kernels in dq8_kernels.hip.
 #include "../../include/dq8.h"
 #include "dq8_internal.h"
+#include "dq8_st.h"
 
 #include <algorithm>
 #include <new>
@@ -18,6 +19,10 @@ struct dq8_ctx {
   void* chain = nullptr;
   size_t chain_bytes = 0;
   uint32_t* flag = nullptr;  // non-finite flag for synchronous checks
+  // Two pinned host buffers through which weight loads stream to the device,
+  // and the events of the copies out of them (created on first use).
+  void* staging[2] = {nullptr, nullptr};
+  hipEvent_t staged[2] = {nullptr, nullptr};
 };
 
 struct dq8_weights {
@@ -294,6 +299,85 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
   return DQ8_OK;
 }
 
+// ------------------------------------------------------------- weight loads
+
+constexpr size_t kStagingBytes = 8u << 20;
+
+// Copies `bytes` bytes of a host source to device memory dst through the
+// context's two pinned staging buffers: fill(buffer, offset, count) writes
+// source bytes [offset, offset + count) into a buffer (a memcpy or a file
+// read) while the other buffer's copy is in flight.  On failure, copies
+// already queued may still be running: the caller synchronizes `s` before it
+// frees dst.
+template <typename Fill>
+dq8_status stage_to_device(dq8_ctx* ctx, uint8_t* dst, size_t bytes, hipStream_t s, Fill fill) {
+  for (int b = 0; b < 2; ++b) {
+    if (!ctx->staging[b]) {
+      hipError_t e = hipHostMalloc(&ctx->staging[b], kStagingBytes, hipHostMallocDefault);
+      if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->staged[b], hipEventDisableTiming);
+      if (e != hipSuccess) return from_hip(e);
+    } else if (hipEventSynchronize(ctx->staged[b]) != hipSuccess) {  // an earlier load's copy
+      return DQ8_ERR_DEVICE;
+    }
+  }
+  size_t i = 0;
+  for (size_t off = 0; off < bytes; off += kStagingBytes, ++i) {
+    const int b = (int)(i & 1);
+    const size_t count = std::min(kStagingBytes, bytes - off);
+    if (i >= 2 && hipEventSynchronize(ctx->staged[b]) != hipSuccess) return DQ8_ERR_DEVICE;
+    if (!fill(ctx->staging[b], off, count)) return DQ8_ERR_IO;
+    hipError_t e = hipMemcpyAsync(dst + off, ctx->staging[b], count, hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = hipEventRecord(ctx->staged[b], s);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  return DQ8_OK;
+}
+
+size_t raw_element_bytes(int dtype) { return dtype == dq8::kDtypeF32 ? 4 : 2; }
+bool raw_shape_ok(size_t n, size_t k) { return n && k && n <= (1u << 30) && k <= (1u << 30) && n * k <= ((size_t)1 << 40); }
+
+// Data::quantize of n*k stored elements at device address raw (weights.rs:98-146),
+// then the repack into a new handle.  Non-finite elements: DQ8_ERR_NONFINITE,
+// as Data::read's "non-finite weights" (weights.rs:170-187).
+dq8_status quantize_raw_weights(dq8_ctx* ctx, const void* raw, int dtype, size_t n, size_t k, hipStream_t s,
+                                dq8_weights** out) {
+  const size_t g = groups_of(k);
+  uint8_t* values = nullptr;
+  float* scales = nullptr;
+  uint32_t flag = 0;
+  hipError_t e = hipMalloc(&values, n * k);
+  if (e == hipSuccess) e = hipMalloc(&scales, n * g * sizeof(float));
+  if (e == hipSuccess) e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
+  if (e == hipSuccess)
+    e = dq8::launch_quantize_raw(raw, dtype, (int)n, (int)k, (int8_t*)values, (int)k, scales, (int)g, ctx->flag, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(&flag, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  dq8_status st = from_hip(e);
+  if (st == DQ8_OK && flag) st = DQ8_ERR_NONFINITE;
+  if (st == DQ8_OK) st = dq8_weights_from_quantized(ctx, values, scales, n, k, s, out);
+  (void)hipStreamSynchronize(s);
+  (void)hipFree(values);
+  (void)hipFree(scales);
+  return st;
+}
+
+// Stream n*k stored elements from a host source into a device buffer, then
+// quantize and repack them.
+template <typename Fill>
+dq8_status load_weights(dq8_ctx* ctx, int dtype, size_t n, size_t k, hipStream_t s, dq8_weights** out, Fill fill) {
+  const size_t bytes = n * k * raw_element_bytes(dtype);
+  uint8_t* raw = nullptr;
+  hipError_t e = hipMalloc(&raw, bytes);
+  if (e != hipSuccess) return from_hip(e);
+  dq8_status st = stage_to_device(ctx, raw, bytes, s, fill);
+  if (st == DQ8_OK) st = quantize_raw_weights(ctx, raw, dtype, n, k, s, out);
+  (void)hipStreamSynchronize(s);
+  (void)hipFree(raw);
+  return st;
+}
+
+bool dtype_ok(dq8_dtype d) { return d == DQ8_F32 || d == DQ8_BF16 || d == DQ8_F16; }
+
 }  // namespace
 
 extern "C" {
@@ -306,6 +390,8 @@ const char* dq8_status_string(dq8_status s) {
     case DQ8_ERR_ARG: return "invalid argument";
     case DQ8_ERR_DEVICE: return "device error";
     case DQ8_ERR_NOMEM: return "out of device memory";
+    case DQ8_ERR_FORMAT: return "invalid safetensors data";
+    case DQ8_ERR_IO: return "file read failed";
   }
   return "unknown status";
 }
@@ -336,6 +422,10 @@ dq8_status dq8_destroy(dq8_ctx* ctx) {
   (void)hipFree(ctx->work);
   (void)hipFree(ctx->chain);
   (void)hipFree(ctx->flag);
+  for (int b = 0; b < 2; ++b) {
+    if (ctx->staged[b]) (void)hipEventDestroy(ctx->staged[b]);
+    if (ctx->staging[b]) (void)hipHostFree(ctx->staging[b]);
+  }
   delete ctx;
   return DQ8_OK;
 }
@@ -379,6 +469,42 @@ dq8_status dq8_weights_from_f32(dq8_ctx* ctx, const float* w, size_t n, size_t k
   (void)hipFree(values);
   (void)hipFree(scales);
   return st;
+}
+
+dq8_status dq8_weights_from_raw(dq8_ctx* ctx, const void* data, dq8_dtype dtype, size_t n, size_t k, void* stream,
+                                dq8_weights** out) {
+  if (!ctx || !data || !out || !dtype_ok(dtype)) return DQ8_ERR_ARG;
+  *out = nullptr;
+  if (!raw_shape_ok(n, k)) return DQ8_ERR_SHAPE;
+  DeviceGuard guard(ctx->device);
+  return quantize_raw_weights(ctx, data, (int)dtype, n, k, (hipStream_t)stream, out);
+}
+
+dq8_status dq8_weights_upload(dq8_ctx* ctx, const void* data_host, dq8_dtype dtype, size_t n, size_t k,
+                              void* stream, dq8_weights** out) {
+  if (!ctx || !data_host || !out || !dtype_ok(dtype)) return DQ8_ERR_ARG;
+  *out = nullptr;
+  if (!raw_shape_ok(n, k)) return DQ8_ERR_SHAPE;
+  DeviceGuard guard(ctx->device);
+  const uint8_t* src = static_cast<const uint8_t*>(data_host);
+  return load_weights(ctx, (int)dtype, n, k, (hipStream_t)stream, out, [&](void* buf, size_t off, size_t count) {
+    memcpy(buf, src + off, count);
+    return true;
+  });
+}
+
+dq8_status dq8_st_load_weights(dq8_ctx* ctx, const dq8_st* st, size_t i, void* stream, dq8_weights** out) {
+  if (!ctx || !st || !out || i >= st->tensors.size()) return DQ8_ERR_ARG;
+  *out = nullptr;
+  const dq8_st_tensor& t = st->tensors[i];
+  const int dtype = dq8::st_dtype_code(t.dtype);
+  if (dtype < 0) return DQ8_ERR_FORMAT;  // "unsupported weight dtype"
+  // weights.rs:346-355: a 2-D projection weight with a non-zero width
+  if (t.shape.size() != 2 || !raw_shape_ok(t.shape[0], t.shape[1])) return DQ8_ERR_SHAPE;
+  DeviceGuard guard(ctx->device);
+  const uint64_t base = st->data_start + t.begin;
+  return load_weights(ctx, dtype, t.shape[0], t.shape[1], (hipStream_t)stream, out,
+                      [&](void* buf, size_t off, size_t count) { return dq8::st_pread(st, buf, count, base + off); });
 }
 
 dq8_status dq8_weights_export(dq8_ctx* ctx, const dq8_weights* w, uint8_t* values, float* scales, void* stream) {

@@ -11,6 +11,8 @@ constexpr int kGroup = 64;        // reference group width (weights.rs:119, tens
 constexpr int kFragBytes = 1024;  // one MFMA operand fragment: 64 lanes x 16 bytes
 constexpr int kMaxBatch = 16;     // projections per launch
 constexpr int kColPad = 256;      // weights are padded to a multiple of this many outputs
+// Stored element types of raw weights (values of dq8_dtype).
+constexpr int kDtypeF32 = 0, kDtypeBF16 = 1, kDtypeF16 = 2;
 
 // Repacked weights, owned by a dq8_weights handle.
 //   values: [Np/32][G][2][64 lanes][16 bytes]; fragment (nb, g, h) holds, at lane l,
@@ -59,6 +61,9 @@ struct Batch {
 // scales row stride lds >= G = ceil(k / 64)
 hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
                            uint32_t* nonfinite, hipStream_t s);
+// The same over raw stored elements of type dtype (kDtype*), decoded exactly.
+hipError_t launch_quantize_raw(const void* x, int dtype, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
+                               uint32_t* nonfinite, hipStream_t s);
 hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int k, Weights* w, hipStream_t s);
 hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipStream_t s);
 hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ldq, hipStream_t s);

@@ -188,13 +188,44 @@ __device__ __forceinline__ V lora_term16(const V& base, const V& zero, int rank,
 }
 
 // ---------------------------------------------------------------------------
+// Stored weight elements (Data::read, weights.rs:147-195): little-endian F32,
+// BF16 (the upper half of an F32) or F16.  Both 16-bit decodings are exact:
+// bf16 -> f32 is f32::from_bits(v << 16) (weights.rs:38-41) and f16 -> f32 is
+// the IEEE conversion that `half` (weights.rs:367-382) spells out.
+template <int DT>
+__device__ __forceinline__ float decode(const void* base, size_t i) {
+  if constexpr (DT == kDtypeF32) {
+    return static_cast<const float*>(base)[i];
+  } else {
+    const uint16_t h = static_cast<const uint16_t*>(base)[i];
+    if constexpr (DT == kDtypeBF16) return __builtin_bit_cast(float, (uint32_t)h << 16);
+    else return (float)__builtin_bit_cast(_Float16, h);
+  }
+}
+template <int DT>
+__device__ __forceinline__ void decode4(const void* base, size_t i, float (&v)[4]) {
+  if constexpr (DT == kDtypeF32) {
+    const float4 t = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  } else {
+    const uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + i);
+    const uint16_t h[4] = {(uint16_t)t.x, (uint16_t)(t.x >> 16), (uint16_t)t.y, (uint16_t)(t.y >> 16)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = decode<DT>(h, j);
+  }
+}
+
 // Quantization: QuantizedInputs::new (tensor.rs:321-339) and the 8-bit
 // Data::quantize (weights.rs:117-136).  One wave covers 256 consecutive
 // elements of a row (4 per lane, 4 groups per wave); a group's absmax is a
 // max-reduction over its 16 lanes.  The division is the IEEE one and roundf
-// rounds half away from zero, as f32::round.
-__global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, int rows, int k, int8_t* __restrict__ q,
+// rounds half away from zero, as f32::round.  x holds DT elements; a
+// non-finite one ORs 1 into *nonfinite (Data::read rejects it for weights,
+// QuantizedInputs::new returns None for inputs).
+template <int DT>
+__global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, int rows, int k, int8_t* __restrict__ q,
                                                   int ldq, float* __restrict__ scales, int lds, uint32_t* nonfinite) {
+  constexpr int ES = DT == kDtypeF32 ? 4 : 2;  // element bytes
   const int lane = threadIdx.x & 63;
   const int chunks = (k + 255) >> 8;
   const long item = (long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -202,14 +233,13 @@ __global__ __launch_bounds__(256) void k_quantize(const float* __restrict__ x, i
   const int row = (int)(item / chunks);
   const int chunk = (int)(item - (long)row * chunks);
   const int k0 = chunk * 256 + lane * 4;
-  const float* xr = x + (size_t)row * k;
+  const size_t r0 = (size_t)row * k;
   float v[4];
-  if ((k & 3) == 0 && k0 + 3 < k && ((uintptr_t)x & 15) == 0) {
-    float4 t = *reinterpret_cast<const float4*>(xr + k0);
-    v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+  if ((k & 3) == 0 && k0 + 3 < k && ((uintptr_t)x & (4 * ES - 1)) == 0) {
+    decode4<DT>(x, r0 + k0, v);
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (k0 + i < k) ? xr[k0 + i] : 0.0f;
+    for (int i = 0; i < 4; ++i) v[i] = (k0 + i < k) ? decode<DT>(x, r0 + k0 + i) : 0.0f;
   }
   bool bad = false;
   float m = 0.0f;
@@ -1226,12 +1256,20 @@ hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int ran
 }
 
 
-hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
-                           uint32_t* nonfinite, hipStream_t s) {
+hipError_t launch_quantize_raw(const void* x, int dtype, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
+                               uint32_t* nonfinite, hipStream_t s) {
   const long waves = (long)rows * ((k + 255) / 256);
   if (waves == 0) return hipSuccess;
-  k_quantize<<<blocks_for(waves, 4), 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
+  const int blocks = blocks_for(waves, 4);
+  if (dtype == kDtypeBF16) k_quantize<kDtypeBF16><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
+  else if (dtype == kDtypeF16) k_quantize<kDtypeF16><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
+  else k_quantize<kDtypeF32><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
   return hipGetLastError();
+}
+
+hipError_t launch_quantize(const float* x, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
+                           uint32_t* nonfinite, hipStream_t s) {
+  return launch_quantize_raw(x, kDtypeF32, rows, k, q, ldq, scales, lds, nonfinite, s);
 }
 
 hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int k, Weights* w, hipStream_t s) {

@@ -10,6 +10,9 @@ The names mirror decider-engine's int8 path:
   Context.quantize       QuantizedInputs::new (None -> NonFinite) tensor.rs:315-353
   Context.linear         linear_int8 + write_columns/Epilogue     tensor.rs:379-456, 272-288
   Context.linear_f32in   linear (quantize + multiply)             tensor.rs:290-308
+  Context.weights_from_raw / weights_upload
+                         Data::read + Data::quantize              weights.rs:147-195, 98-146
+  SafeTensors            read_tensors' checkpoint reader          weights.rs:298-365
 There is no CPU fallback: without libdq8.so, or without a GPU, calls raise.
 """
 from __future__ import annotations
@@ -23,7 +26,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libdq8.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "dq8.h")
 
-OK, ERR_SHAPE, ERR_NONFINITE, ERR_ARG, ERR_DEVICE, ERR_NOMEM = range(6)
+OK, ERR_SHAPE, ERR_NONFINITE, ERR_ARG, ERR_DEVICE, ERR_NOMEM, ERR_FORMAT, ERR_IO = range(8)
+F32, BF16, F16 = 0, 1, 2  # dq8_dtype
 WRITE, ADD, SWIGLU = 0, 1, 2
 ROWS, COLUMNS = 0, 1
 GROUP = 64
@@ -115,6 +119,17 @@ def lib() -> ctypes.CDLL:
         "dq8_ffn": ([_vp, ctypes.POINTER(_FfnWeights), _vp, _vp, _sz, _vp, _vp, _vp, _vp], _i),
         "dq8_group_dots": ([_vp, _vp, _vp, _sz, _vp, _vp], _i),
         "dq8_status_string": ([_i], ctypes.c_char_p),
+        "dq8_weights_from_raw": ([_vp, _vp, _i, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
+        "dq8_weights_upload": ([_vp, _vp, _i, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
+        "dq8_st_open": ([ctypes.c_char_p, ctypes.POINTER(_vp)], _i),
+        "dq8_st_close": ([_vp], _i),
+        "dq8_st_count": ([_vp, ctypes.POINTER(_sz)], _i),
+        "dq8_st_info": ([_vp, _sz, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p),
+                         ctypes.POINTER(_sz), ctypes.POINTER(ctypes.POINTER(_sz)), ctypes.POINTER(_sz)], _i),
+        "dq8_st_find": ([_vp, ctypes.c_char_p, ctypes.POINTER(_sz)], _i),
+        "dq8_st_read_host": ([_vp, _sz, _vp, _sz], _i),
+        "dq8_st_read_f32_host": ([_vp, _sz, _vp, _sz], _i),
+        "dq8_st_load_weights": ([_vp, _vp, _sz, _vp, ctypes.POINTER(_vp)], _i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -261,6 +276,36 @@ class Context:
         h = ctypes.c_void_p()
         _check(lib().dq8_weights_from_quantized(self.handle, values.data_ptr(), scales.data_ptr(), n, k,
                                                 _stream(self.device), ctypes.byref(h)), "dq8_weights_from_quantized")
+        return Weights(self, h.value, n, k)
+
+    def weights_from_raw(self, data, dtype: int | None = None) -> Weights:
+        """Data::read + Data::quantize of stored elements already on the device:
+        a [n][k] float32, bfloat16 or float16 tensor, or uint16 bit patterns
+        with dtype BF16 or F16.  Raises NonFinite for non-finite weights."""
+        torch = _torch()
+        code = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}.get(data.dtype, dtype)
+        if code is None or (data.dtype == torch.uint16 and dtype not in (BF16, F16)):
+            raise ValueError("weights_from_raw: float32/bfloat16/float16 data, or uint16 with dtype BF16/F16")
+        self._dev(data, data.dtype, name="data")
+        n, k = data.shape
+        h = ctypes.c_void_p()
+        _check(lib().dq8_weights_from_raw(self.handle, data.data_ptr(), code, n, k, _stream(self.device),
+                                          ctypes.byref(h)), "dq8_weights_from_raw")
+        return Weights(self, h.value, n, k)
+
+    def weights_upload(self, data, dtype: int) -> Weights:
+        """weights_from_raw from host memory: a C-contiguous 2-D numpy array of
+        stored elements (float32 for F32, uint16 bit patterns for BF16/F16),
+        streamed through the context's pinned staging buffers."""
+        import numpy as np
+
+        want = np.float32 if dtype == F32 else np.uint16
+        if not isinstance(data, np.ndarray) or data.dtype != want or data.ndim != 2 or not data.flags.c_contiguous:
+            raise ValueError(f"weights_upload: a C-contiguous 2-D {np.dtype(want).name} array")
+        n, k = data.shape
+        h = ctypes.c_void_p()
+        _check(lib().dq8_weights_upload(self.handle, data.ctypes.data, dtype, n, k, _stream(self.device),
+                                        ctypes.byref(h)), "dq8_weights_upload")
         return Weights(self, h.value, n, k)
 
     # -- activations ---------------------------------------------------
@@ -442,3 +487,88 @@ class Context:
         _check(lib().dq8_group_dots(self.handle, w.handle, q.data_ptr(), m, dots.data_ptr(), _stream(self.device)),
                "dq8_group_dots")
         return dots
+
+
+def is_projection(name: str, shape) -> bool:
+    """read_tensors' rule for weights quantized at load (weights.rs:346-351),
+    applied to a name with the file's prefix already removed."""
+    return name.startswith("layers.") and "_proj" in name and name.endswith(".weight") and len(shape) == 2
+
+
+class SafeTensors:
+    """One safetensors file through dq8_st_* (the checks of read_tensors,
+    weights.rs:298-365).  Opening and reading need no GPU; load_weights does."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        _check(lib().dq8_st_open(os.fsencode(path), ctypes.byref(h)), f"dq8_st_open({path})")
+        self.handle = h.value
+        n = ctypes.c_size_t()
+        _check(lib().dq8_st_count(self.handle, ctypes.byref(n)), "dq8_st_count")
+        self.tensors = []  # (name, dtype, shape, bytes) in file order
+        for i in range(n.value):
+            name, dt = ctypes.c_char_p(), ctypes.c_char_p()
+            nd, nb = ctypes.c_size_t(), ctypes.c_size_t()
+            shp = ctypes.POINTER(ctypes.c_size_t)()
+            _check(lib().dq8_st_info(self.handle, i, ctypes.byref(name), ctypes.byref(dt), ctypes.byref(nd),
+                                     ctypes.byref(shp), ctypes.byref(nb)), "dq8_st_info")
+            self.tensors.append((name.value.decode(), dt.value.decode(), tuple(shp[j] for j in range(nd.value)),
+                                 nb.value))
+        self._index = {t[0]: i for i, t in enumerate(self.tensors)}
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().dq8_st_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def names(self):
+        return [t[0] for t in self.tensors]
+
+    def info(self, name: str):
+        """(dtype, shape, bytes) of a tensor."""
+        return self.tensors[self._index[name]][1:]
+
+    def read(self, name: str):
+        """Data::read: the stored elements (float32, or uint16 bit patterns for
+        BF16/F16), shaped.  Raises NonFinite for non-finite weights."""
+        import numpy as np
+
+        i = self._index[name]
+        _, dt, shape, nbytes = self.tensors[i]
+        out = np.empty(shape, dtype=np.float32 if dt == "F32" else np.uint16)
+        if out.nbytes != nbytes and dt in ("F32", "BF16", "F16"):
+            raise Dq8Error(ERR_SHAPE, "read")
+        _check(lib().dq8_st_read_host(self.handle, i, out.ctypes.data, nbytes), f"dq8_st_read_host({name})")
+        return out
+
+    def read_f32(self, name: str):
+        """Data::into_f32 of a tensor, shaped."""
+        import numpy as np
+
+        i = self._index[name]
+        shape = self.tensors[i][2]
+        out = np.empty(shape, dtype=np.float32)
+        _check(lib().dq8_st_read_f32_host(self.handle, i, out.ctypes.data, out.size), f"dq8_st_read_f32_host({name})")
+        return out
+
+    def load_weights(self, ctx: "Context", name: str) -> "Weights":
+        """A projection weight [n][k] from the file to the device, quantized and repacked."""
+        i = self._index[name]
+        _, _, shape, _ = self.tensors[i]
+        h = ctypes.c_void_p()
+        _check(lib().dq8_st_load_weights(ctx.handle, self.handle, i, _stream(ctx.device), ctypes.byref(h)),
+               f"dq8_st_load_weights({name})")
+        return Weights(ctx, h.value, shape[0], shape[1])

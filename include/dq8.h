@@ -42,8 +42,14 @@ typedef enum dq8_status {
     DQ8_ERR_NONFINITE = 2, /* QuantizedInputs::new returned None: caller takes its FP32 path */
     DQ8_ERR_ARG = 3,       /* null handle/pointer, bad enum value or misaligned pointer */
     DQ8_ERR_DEVICE = 4,    /* a HIP call failed */
-    DQ8_ERR_NOMEM = 5      /* device allocation failed */
+    DQ8_ERR_NOMEM = 5,     /* device allocation failed */
+    DQ8_ERR_FORMAT = 6,    /* a safetensors file or tensor that read_tensors / Data::read rejects */
+    DQ8_ERR_IO = 7         /* a file could not be opened or read */
 } dq8_status;
+
+/* Stored element types of weights (Data::{F32, Bf16, F16}, weights.rs:12-15),
+ * little-endian as in safetensors files. */
+typedef enum dq8_dtype { DQ8_F32 = 0, DQ8_BF16 = 1, DQ8_F16 = 2 } dq8_dtype;
 
 /* Epilogue::{Write, Add, SwiGlu} (tensor.rs:85-100). */
 typedef enum dq8_epilogue { DQ8_WRITE = 0, DQ8_ADD = 1, DQ8_SWIGLU = 2 } dq8_epilogue;
@@ -74,6 +80,21 @@ dq8_status dq8_weights_from_f32(dq8_ctx *ctx, const float *w, size_t n, size_t k
  * host; only the repack runs here. */
 dq8_status dq8_weights_from_quantized(dq8_ctx *ctx, const uint8_t *values, const float *scales, size_t n,
                                       size_t k, void *stream, dq8_weights **out);
+
+/* Data::read + Data::quantize(width, Precision::Int8Compute) of one projection
+ * weight (weights.rs:147-195, 98-146, 346-355) from its stored elements: data
+ * holds n*k elements of `dtype` in device memory.  Any non-finite element
+ * returns DQ8_ERR_NONFINITE and no handle ("non-finite weights").  Elements are
+ * decoded exactly (BF16: the upper half of an f32; F16: the IEEE conversion of
+ * `half`, weights.rs:367-382), quantized in groups of 64 and repacked on the
+ * device.  Synchronizes `stream`. */
+dq8_status dq8_weights_from_raw(dq8_ctx *ctx, const void *data, dq8_dtype dtype, size_t n, size_t k, void *stream,
+                                dq8_weights **out);
+/* dq8_weights_from_raw with the elements in host memory (a read buffer or a
+ * file mapping): they are streamed to the device through the context's two
+ * pinned staging buffers, each refilled while the other one's copy runs. */
+dq8_status dq8_weights_upload(dq8_ctx *ctx, const void *data_host, dq8_dtype dtype, size_t n, size_t k,
+                              void *stream, dq8_weights **out);
 
 /* Write the handle's weights back in the Data::Quantized layout (for checks). */
 dq8_status dq8_weights_export(dq8_ctx *ctx, const dq8_weights *w, uint8_t *values, float *scales,
@@ -193,6 +214,48 @@ dq8_status dq8_group_dots(dq8_ctx *ctx, const dq8_weights *w, const int8_t *q, s
 
 /* Human-readable name of a status. */
 const char *dq8_status_string(dq8_status s);
+
+/* ---------------------------------------------------------------- safetensors
+ * The checkpoint reader of read_tensors (weights.rs:298-365) over one file.
+ * dq8_st_open reads and checks the header as read_tensors does with the
+ * metadata rules of the safetensors crate 0.8.0 (Cargo.lock):
+ *   - an 8-byte little-endian header size of at most 16 MiB, with the header
+ *     inside the file;
+ *   - a JSON object mapping tensor names to {"dtype", "shape", "data_offsets"},
+ *     plus an optional "__metadata__" object of strings; a repeated key keeps
+ *     its last value;
+ *   - tensors ordered by data_offsets must tile the data section from 0
+ *     without gaps or overlaps, each spanning exactly its shape's bytes;
+ *   - the data section must end exactly at the end of the file.
+ * Any violation returns DQ8_ERR_FORMAT (DQ8_ERR_IO if the file cannot be
+ * read).  No tensor data is read by dq8_st_open.  Tensors are indexed in
+ * file order (ascending data offsets, as Metadata::offset_keys).  Name, dtype
+ * and shape pointers stay valid until dq8_st_close.  The host-only calls
+ * (all but dq8_st_load_weights) need no GPU. */
+typedef struct dq8_st dq8_st;
+dq8_status dq8_st_open(const char *path, dq8_st **out);
+dq8_status dq8_st_close(dq8_st *st);
+dq8_status dq8_st_count(const dq8_st *st, size_t *count);
+/* Tensor i: name, dtype as written in the file ("F32", "BF16", "I8", ...),
+ * rank, shape and byte size. */
+dq8_status dq8_st_info(const dq8_st *st, size_t i, const char **name, const char **dtype, size_t *ndim,
+                       const size_t **shape, size_t *bytes);
+/* Index of the tensor named `name` (DQ8_ERR_ARG if there is none). */
+dq8_status dq8_st_find(const dq8_st *st, const char *name, size_t *index);
+/* Data::read (weights.rs:147-195): tensor i's elements as stored, into host
+ * memory dst of exactly its byte size.  Only F32, BF16 and F16 tensors can be
+ * read (DQ8_ERR_FORMAT otherwise, "unsupported weight dtype"); a non-finite
+ * element returns DQ8_ERR_NONFINITE ("non-finite weights"). */
+dq8_status dq8_st_read_host(const dq8_st *st, size_t i, void *dst_host, size_t bytes);
+/* Data::into_f32 (weights.rs:83-90) of tensor i into host memory: count must
+ * equal its element count.  Same errors as dq8_st_read_host. */
+dq8_status dq8_st_read_f32_host(const dq8_st *st, size_t i, float *dst_host, size_t count);
+/* A projection weight (a 2-D F32/BF16/F16 tensor [n][k], k > 0, quantized at
+ * load by weights.rs:346-355) straight from the file to a dq8_weights handle:
+ * read into pinned staging, copied to the device, decoded, checked,
+ * quantized and repacked there (dq8_weights_from_raw).  DQ8_ERR_SHAPE for
+ * other ranks or k == 0. */
+dq8_status dq8_st_load_weights(dq8_ctx *ctx, const dq8_st *st, size_t i, void *stream, dq8_weights **out);
 
 #ifdef __cplusplus
 }

@@ -93,6 +93,40 @@ def quantize_weights(w: np.ndarray):
     return v, s
 
 
+def decode_weights(raw: np.ndarray, dtype: str) -> np.ndarray:
+    """Data::row / Data::into_f32 of stored elements (weights.rs:35-46, 83-90).
+
+    F32: unchanged.  BF16: f32::from_bits((v as u32) << 16).  F16: `half`
+    (weights.rs:367-382) in float32 arithmetic: sign * m * 2^-24 for e = 0,
+    +-inf / NaN for e = 31, else sign * (1 + m/1024) * 2^(e-15).
+    """
+    if dtype == "F32":
+        return np.ascontiguousarray(raw, dtype=np.float32)
+    v = np.ascontiguousarray(raw, dtype=np.uint16)
+    if dtype == "BF16":
+        return (v.astype(np.uint32) << np.uint32(16)).view(np.float32)
+    if dtype != "F16":
+        raise ValueError(f"unsupported weight dtype {dtype}")
+    sign = np.where(v & 0x8000, np.float32(-1.0), np.float32(1.0))
+    e = ((v >> 10) & 31).astype(np.int32)
+    m = (v & 1023).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        sub = sign * m * np.float32(2.0 ** -24)
+        norm = sign * ((np.float32(1.0) + m / np.float32(1024.0)) * np.ldexp(np.float32(1.0), e - 15).astype(np.float32))
+        special = np.where(m == 0, sign * np.float32(np.inf), np.float32(np.nan))
+    return np.where(e == 0, sub, np.where(e == 31, special, norm)).astype(np.float32)
+
+
+def weights_finite(raw: np.ndarray, dtype: str) -> bool:
+    """Data::read's check (weights.rs:170-187): F32 is_finite, or the 16-bit
+    exponent mask (0x7f80 for BF16, 0x7c00 for F16) not all ones."""
+    if dtype == "F32":  # float32 values, or their uint32 bit patterns
+        raw = np.asarray(raw)
+        return bool(np.all(np.isfinite(raw.view(np.float32) if raw.dtype == np.uint32 else raw.astype(np.float32))))
+    mask = np.uint16(0x7F80 if dtype == "BF16" else 0x7C00)
+    return bool(np.all((np.asarray(raw, dtype=np.uint16) & mask) != mask))
+
+
 def dot(a: np.ndarray, b: np.ndarray) -> int:
     a = np.ascontiguousarray(a, dtype=np.int8)
     b = np.ascontiguousarray(b, dtype=np.uint8)
