@@ -210,8 +210,10 @@ struct QOut {
 // qout (one item only): the item's stored result is then quantized by k_quantize.
 // (Quantizing in the projection's epilogue was measured slower: the projection
 // kernels are VALU-bound, the quantize pass is memory-bound.)
+// unless: the launches do nothing on the device if *unless != 0 (the inputs
+// were not finite; the caller runs the FP32 kernel for these items).
 dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, int32_t* dots, hipStream_t s,
-                      const QOut* qout = nullptr) {
+                      const QOut* qout = nullptr, const uint32_t* unless = nullptr) {
   size_t need = 0;
   for (size_t i = 0; i < count; ++i) {
     if (!items[i].m) continue;
@@ -224,7 +226,10 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     if (st != DQ8_OK) return st;
   }
   dq8::Batch batch[dq8::kKinds];
-  for (dq8::Batch& b : batch) b.count = b.total_waves = b.any_lora = 0;
+  for (dq8::Batch& b : batch) {
+    b.count = b.total_waves = b.any_lora = 0;
+    b.unless = unless;
+  }
   size_t offset = 0;
   // Two passes: projections with long K (more than 32 groups) first, so their
   // blocks start when the launch does instead of trailing the short ones.
@@ -299,6 +304,97 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
   return DQ8_OK;
 }
 
+// ------------------------------------------------------- fp32-input paths
+
+// Arguments of the entry points that take fp32 inputs x [m][k].
+dq8_status check_f32in(const dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t m, const float* out,
+                       dq8_layout layout, dq8_epilogue epilogue, const dq8_lora* lora) {
+  if (!ctx || !w) return DQ8_ERR_ARG;
+  if (m == 0) return DQ8_OK;
+  if (!x || !out) return DQ8_ERR_ARG;
+  if (layout != DQ8_ROWS && layout != DQ8_COLUMNS) return DQ8_ERR_ARG;
+  if (epilogue != DQ8_WRITE && epilogue != DQ8_ADD && epilogue != DQ8_SWIGLU) return DQ8_ERR_ARG;
+  if (layout == DQ8_COLUMNS && epilogue != DQ8_WRITE) return DQ8_ERR_ARG;
+  if (m > (1u << 30)) return DQ8_ERR_SHAPE;
+  if (w->w.device != ctx->device) return DQ8_ERR_ARG;
+  return check_lora(lora);
+}
+
+// Inputs quantized into the context workspace: q with rows of G*64 bytes,
+// scales with rows of a multiple of 4 groups.
+struct WorkInputs {
+  int8_t* q;
+  int ldq;
+  float* xs;
+  int ldxs;
+};
+
+// QuantizedInputs::new of x [m][w.k] into the workspace.  ctx->flag is
+// cleared first and ends up non-zero if x holds a non-finite value.
+dq8_status quantize_to_work(dq8_ctx* ctx, const dq8::Weights& w, const float* x, size_t m, hipStream_t s,
+                            WorkInputs& in) {
+  const size_t ldq = (size_t)w.g * kGroup;
+  const size_t qbytes = (m * ldq + 255) / 256 * 256;
+  dq8_status st = ensure_work(ctx, qbytes + xs_pad_bytes(w, m));
+  if (st != DQ8_OK) return st;
+  in.q = (int8_t*)ctx->work;
+  in.ldq = (int)ldq;
+  in.xs = (float*)((char*)ctx->work + qbytes);
+  in.ldxs = padded_groups(w);
+  hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
+  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, w.k, in.q, in.ldq, in.xs, in.ldxs, ctx->flag, s);
+  return from_hip(e);
+}
+
+// Waits for the stream and reports ctx->flag as DQ8_ERR_NONFINITE.
+dq8_status finish_nonfinite(dq8_ctx* ctx, hipStream_t s) {
+  uint32_t host = 0;
+  hipError_t e = hipMemcpyAsync(&host, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return from_hip(e);
+  return host ? DQ8_ERR_NONFINITE : DQ8_OK;
+}
+
+// The int8 kernels for one projection over workspace inputs.
+dq8_status launch_one(const dq8::Weights& w, const WorkInputs& in, size_t m, const float* bias, const dq8_lora* lora,
+                      float* out, int layout, int epilogue, const uint32_t* unless, hipStream_t s) {
+  dq8::Batch b;
+  b.count = 1;
+  b.total_waves = 0;
+  b.any_lora = lora != nullptr;
+  b.unless = unless;
+  dq8::Proj& p = b.p[0];
+  fill_proj(p, w, in.q, in.ldq, in.xs, in.ldxs, m, bias, out, nullptr, layout, epilogue, lora);
+  const int kind = kind_of(w, m);
+  place_proj(p, kind, b);
+  return from_hip(dq8::launch_linear(b, kind, false, s));
+}
+
+// The FP32 path of a projection (k_linear_fp32) over x [m][w.k].
+dq8::FProj make_fproj(const dq8::Weights& w, const float* x, size_t m, const float* bias, const dq8_lora* lora,
+                      float* out, int layout, int epilogue, const uint32_t* when) {
+  dq8::FProj p;
+  p.x = x;
+  p.wt = w.values;
+  p.wst = w.scales;
+  p.bias = bias;
+  p.lora = lora != nullptr;
+  p.rank = lora ? (int)lora->rank : 0;
+  p.lscale = lora ? lora->scale : 0.0f;
+  p.lmid = lora ? lora->mid : nullptr;
+  p.lb = lora ? lora->b : nullptr;
+  p.out = out;
+  p.m = (int)m;
+  p.k = w.k;
+  p.g = w.g;
+  p.n = w.n;
+  p.np = w.np;
+  p.epilogue = epilogue;
+  p.layout = layout;
+  p.when = when;
+  return p;
+}
+
 // ------------------------------------------------------------- weight loads
 
 constexpr size_t kStagingBytes = 8u << 20;
@@ -347,7 +443,7 @@ dq8_status quantize_raw_weights(dq8_ctx* ctx, const void* raw, int dtype, size_t
   uint32_t flag = 0;
   hipError_t e = hipMalloc(&values, n * k);
   if (e == hipSuccess) e = hipMalloc(&scales, n * g * sizeof(float));
-  if (e == hipSuccess) e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
+  if (e == hipSuccess) e = dq8::launch_fill_u32(ctx->flag, 0, s);
   if (e == hipSuccess)
     e = dq8::launch_quantize_raw(raw, dtype, (int)n, (int)k, (int8_t*)values, (int)k, scales, (int)g, ctx->flag, s);
   if (e == hipSuccess) e = hipMemcpyAsync(&flag, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
@@ -541,7 +637,7 @@ dq8_status dq8_quantize(dq8_ctx* ctx, const float* x, size_t m, size_t k, int8_t
   hipStream_t s = (hipStream_t)stream;
   uint32_t* flag = nonfinite ? nonfinite : ctx->flag;
   hipError_t e = hipSuccess;
-  if (!nonfinite) e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
+  if (!nonfinite) e = dq8::launch_fill_u32(ctx->flag, 0, s);
   if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, (int)k, q, (int)k, scales, (int)groups_of(k), flag, s);
   if (e != hipSuccess) return from_hip(e);
   if (nonfinite) return DQ8_OK;
@@ -609,51 +705,42 @@ dq8_status dq8_linear_batch(dq8_ctx* ctx, const dq8_linear_item* items, size_t c
 
 dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t m, const float* bias,
                             float* out, dq8_layout layout, dq8_epilogue epilogue, void* stream) {
-  if (!ctx || !w) return DQ8_ERR_ARG;
-  if (m == 0) return DQ8_OK;
-  if (!x || !out) return DQ8_ERR_ARG;
-  if (layout != DQ8_ROWS && layout != DQ8_COLUMNS) return DQ8_ERR_ARG;
-  if (epilogue != DQ8_WRITE && epilogue != DQ8_ADD && epilogue != DQ8_SWIGLU) return DQ8_ERR_ARG;
-  if (layout == DQ8_COLUMNS && epilogue != DQ8_WRITE) return DQ8_ERR_ARG;
-  if (m > (1u << 30) || w->w.device != ctx->device) return m > (1u << 30) ? DQ8_ERR_SHAPE : DQ8_ERR_ARG;
+  dq8_status st = check_f32in(ctx, w, x, m, out, layout, epilogue, nullptr);
+  if (st != DQ8_OK || m == 0) return st;
   DeviceGuard guard(ctx->device);
   hipStream_t s = (hipStream_t)stream;
-  const size_t ldq = (size_t)w->w.g * kGroup;
-  const size_t qbytes = (m * ldq + 255) / 256 * 256;
-  const int ldxs = padded_groups(w->w);
-  dq8_status st = ensure_work(ctx, qbytes + xs_pad_bytes(w->w, m));
+  WorkInputs in;
+  st = quantize_to_work(ctx, w->w, x, m, s, in);
   if (st != DQ8_OK) return st;
-  int8_t* q = (int8_t*)ctx->work;
-  float* xs = (float*)((char*)ctx->work + qbytes);
-  hipError_t e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
-  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, w->w.k, q, (int)ldq, xs, ldxs, ctx->flag, s);
-  uint32_t host = 0;
-  if (e == hipSuccess) e = hipMemcpyAsync(&host, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (e != hipSuccess) return from_hip(e);
-  if (host) return DQ8_ERR_NONFINITE;
-  dq8::Batch b;
-  b.count = 1;
-  dq8::Proj& p = b.p[0];
-  fill_proj(p, w->w, q, (int)ldq, xs, ldxs, m, bias, out, nullptr, layout, epilogue, nullptr);
-  b.total_waves = 0;
-  b.any_lora = 0;
-  const int kind = kind_of(w->w, m);
-  place_proj(p, kind, b);
-  return from_hip(dq8::launch_linear(b, kind, false, s));
+  st = finish_nonfinite(ctx, s);
+  if (st != DQ8_OK) return st;
+  return launch_one(w->w, in, m, bias, nullptr, out, layout, epilogue, nullptr, s);
 }
 
-namespace {
-// A result quantization whose non-finite report is synchronous (nonfinite ==
-// NULL): zero the context flag before, read it after.
-dq8_status finish_nonfinite(dq8_ctx* ctx, hipStream_t s) {
-  uint32_t host = 0;
-  hipError_t e = hipMemcpyAsync(&host, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
-  if (e == hipSuccess) e = hipStreamSynchronize(s);
-  if (e != hipSuccess) return from_hip(e);
-  return host ? DQ8_ERR_NONFINITE : DQ8_OK;
+dq8_status dq8_linear_fp32(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t m, const float* bias,
+                           const dq8_lora* lora, float* out, dq8_layout layout, dq8_epilogue epilogue, void* stream) {
+  dq8_status st = check_f32in(ctx, w, x, m, out, layout, epilogue, lora);
+  if (st != DQ8_OK || m == 0) return st;
+  DeviceGuard guard(ctx->device);
+  return from_hip(
+      dq8::launch_linear_fp32(make_fproj(w->w, x, m, bias, lora, out, layout, epilogue, nullptr), (hipStream_t)stream));
 }
-}  // namespace
+
+dq8_status dq8_apply(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t m, const float* bias,
+                     const dq8_lora* lora, float* out, dq8_layout layout, dq8_epilogue epilogue, void* stream) {
+  dq8_status st = check_f32in(ctx, w, x, m, out, layout, epilogue, lora);
+  if (st != DQ8_OK || m == 0) return st;
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = (hipStream_t)stream;
+  WorkInputs in;
+  st = quantize_to_work(ctx, w->w, x, m, s, in);
+  if (st != DQ8_OK) return st;
+  // Both paths are queued; the device flag of the quantization lets exactly
+  // one of them run (tensor.rs:190-201), with no synchronization.
+  st = launch_one(w->w, in, m, bias, lora, out, layout, epilogue, ctx->flag, s);
+  if (st != DQ8_OK) return st;
+  return from_hip(dq8::launch_linear_fp32(make_fproj(w->w, x, m, bias, lora, out, layout, epilogue, ctx->flag), s));
+}
 
 dq8_status dq8_linear_q(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, const float* scales, size_t m,
                         const float* bias, const dq8_lora* lora, float* out, dq8_epilogue epilogue, int8_t* q_out,
@@ -668,7 +755,7 @@ dq8_status dq8_linear_q(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, con
   DeviceGuard guard(ctx->device);
   hipStream_t s = (hipStream_t)stream;
   if (!nonfinite) {
-    hipError_t e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
+    hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
     if (e != hipSuccess) return from_hip(e);
   }
   QOut qo = {q_out, scales_out, nonfinite ? nonfinite : ctx->flag};
@@ -702,33 +789,35 @@ dq8_status dq8_ffn(dq8_ctx* ctx, const dq8_ffn_weights* f, const int8_t* q, cons
   int8_t* qh = (int8_t*)ctx->chain;
   float* sh = (float*)((char*)ctx->chain + qbytes);
   float* mid = (float*)((char*)ctx->chain + qbytes + sbytes);
-  if (!nonfinite) {
-    hipError_t e = hipMemsetAsync(ctx->flag, 0, sizeof(uint32_t), s);
-    if (e != hipSuccess) return from_hip(e);
-  }
+  hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
+  if (e != hipSuccess) return from_hip(e);
   // gate: Write into h (qwen.rs:489); up: SwiGlu into h, quantized on the fly (qwen.rs:490-491)
   dq8_linear_item gi = {f->gate, q, scales, m, f->gate_bias, h, DQ8_ROWS, DQ8_WRITE, f->gate_lora};
   st = run_linear(ctx, &gi, 1, nullptr, s);
   if (st != DQ8_OK) return st;
-  QOut qo = {qh, sh, nonfinite ? nonfinite : ctx->flag};
+  QOut qo = {qh, sh, ctx->flag};
   dq8_linear_item ui = {f->up, q, scales, m, f->up_bias, h, DQ8_ROWS, DQ8_SWIGLU, f->up_lora};
   st = run_linear(ctx, &ui, 1, nullptr, s, &qo);
   if (st != DQ8_OK) return st;
-  if (!nonfinite) {
-    // QuantizedInputs::new(h) returned None: the crate's down projection takes its
-    // FP32 path on h (tensor.rs:197-201), which is the caller's to run.
-    st = finish_nonfinite(ctx, s);
-    if (st != DQ8_OK) return st;
-  }
-  // down: Add into the residual (qwen.rs:492), its adapter's middle product from h
-  dq8_lora dl = {mid, f->down_lora_b, rank, f->down_lora_scale};
-  if (rank > 0) {
-    hipError_t e = dq8::launch_lora_mid(h, (int)m, (int)inter, f->down_lora_a, (int)rank, mid, s);
+  if (nonfinite) {
+    e = dq8::launch_or_u32(nonfinite, ctx->flag, s);
     if (e != hipSuccess) return from_hip(e);
   }
-  dq8_linear_item di = {f->down, qh, sh, m, f->down_bias, residual, DQ8_ROWS, DQ8_ADD,
-                        f->down_lora_a ? &dl : nullptr};
-  return run_linear(ctx, &di, 1, nullptr, s);
+  // down: Add into the residual (qwen.rs:492), its adapter's middle product from h.
+  // If h holds a non-finite value, QuantizedInputs::new(h) is None and the crate
+  // takes the FP32 path on h (tensor.rs:197-201): both are queued and the flag
+  // lets exactly one of them run on the device.
+  dq8_lora dl = {mid, f->down_lora_b, rank, f->down_lora_scale};
+  if (rank > 0) {
+    e = dq8::launch_lora_mid(h, (int)m, (int)inter, f->down_lora_a, (int)rank, mid, s);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  const dq8_lora* dlp = f->down_lora_a ? &dl : nullptr;
+  dq8_linear_item di = {f->down, qh, sh, m, f->down_bias, residual, DQ8_ROWS, DQ8_ADD, dlp};
+  st = run_linear(ctx, &di, 1, nullptr, s, nullptr, ctx->flag);
+  if (st != DQ8_OK) return st;
+  return from_hip(
+      dq8::launch_linear_fp32(make_fproj(d, h, m, f->down_bias, dlp, residual, DQ8_ROWS, DQ8_ADD, ctx->flag), s));
 }
 
 dq8_status dq8_group_dots(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, size_t m, int32_t* dots,

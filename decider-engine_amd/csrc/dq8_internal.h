@@ -55,6 +55,26 @@ struct Batch {
   int count;
   int total_waves;  // blocks of the launch
   int any_lora;     // some projection has a LoRA adapter (selects the kernels with the LoRA epilogue)
+  // When set, the launch does nothing if *unless != 0: the inputs were not
+  // finite and the FP32 kernel (k_linear_fp32) computes these outputs instead.
+  const uint32_t* unless;
+};
+
+// One projection of the FP32 path (Projection::columns_tiled, tensor.rs:206-269)
+// over fp32 inputs x [m][k] and dequantized int8 weights.
+struct FProj {
+  const float* x;
+  const uint8_t* wt;  // Weights::values
+  const float* wst;   // Weights::scales
+  const float* bias;  // [n] or null
+  const float* lmid;  // LoRA middle product [m][rank] (rank > 0)
+  const float* lb;    // LoRA B [n][rank]
+  int lora, rank;
+  float lscale;
+  float* out;
+  int m, k, g, n, np;
+  int epilogue, layout;
+  const uint32_t* when;  // if set, the launch does nothing unless *when != 0
 };
 
 // Kernel launchers (dq8_kernels.hip).  All return hipError_t of the launch.
@@ -68,6 +88,12 @@ hipError_t launch_repack(const uint8_t* values, const float* scales, int n, int 
 hipError_t launch_export(const Weights* w, uint8_t* values, float* scales, hipStream_t s);
 hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ldq, hipStream_t s);
 hipError_t launch_pad_scales(const float* xs, int rows, int g, float* dst, int ld, hipStream_t s);
+// *p = v, as a kernel (graph-capturable, unlike a memset node).
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t s);
+// *dst |= *src on the device.
+hipError_t launch_or_u32(uint32_t* dst, const uint32_t* src, hipStream_t s);
+// The FP32 path of a projection (see FProj).
+hipError_t launch_linear_fp32(const FProj& p, hipStream_t s);
 // LoRA middle product mid [m][rank] = dot_scores(x_r, a_j) + 0.0 (x [m][k], a [rank][k]).
 hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int rank, float* mid, hipStream_t s);
 // Kind: 0 wide (M > 32), 1 skinny (M <= 16), 2 skinny (16 < M <= 32).  dots

@@ -501,6 +501,7 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   __shared__ __attribute__((aligned(16))) Stage stg[STAGES];
   __shared__ __attribute__((aligned(16))) XChunk xc[DOTS ? 1 : 2];
   auto stage = [&](int i) -> Stage& { return stg[i]; };
+  if (b.unless && *b.unless) return;  // non-finite inputs: the FP32 kernel runs instead
 
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
@@ -1156,6 +1157,7 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
 template <int RT, int CT, int CTL, int DBS, int DBL, bool DOTS, bool LORA>
 __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[skinny_lds_bytes(RT, CTL)];
+  if (b.unless && *b.unless) return;  // non-finite inputs: the FP32 kernel runs instead
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const Proj& P = b.p[find_proj(b, blockIdx.x)];
@@ -1244,9 +1246,155 @@ __global__ __launch_bounds__(256) void k_lora_mid(const float* __restrict__ x, i
   }
 }
 
+// dot_scores (tensor.rs:6-25, the x86-64 order) of a[0..len) and b[0..len)
+// from plain memory: eight lane sums over the full chunks of 8, added in
+// order from -0.0, then the tail elements one by one; no fused multiply-add.
+__device__ __forceinline__ float dot_scores_rows(const float* a, const float* b, int len) {
+  const int chunks = len >> 3;
+  float lanes[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = 0; c < chunks; ++c)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) lanes[q] = lanes[q] + a[8 * c + q] * b[8 * c + q];
+  float sum = -0.0f;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) sum = sum + lanes[q];
+  for (int t = 8 * chunks; t < len; ++t) sum = sum + a[t] * b[t];
+  return sum;
+}
+
+// Weight element (n, t) of the repacked layout, dequantized as Data::row does
+// for 8-bit Quantized data (weights.rs:47-78): (float)(int8)q * scale.
+__device__ __forceinline__ float dequant(const FProj& P, int n, int t) {
+  const int g = t >> 6, off = t & 63, h = off >> 5, part = (off >> 4) & 1;
+  const int8_t q = (int8_t)P.wt[((size_t)((n >> 5) * P.g + g) * 2 + h) * kFragBytes + ((n & 31) + 32 * part) * 16 +
+                                (off & 15)];
+  return (float)q * P.wst[(size_t)g * P.np + n];
+}
+
+// The FP32 path of a projection, Projection::columns_tiled (tensor.rs:206-269),
+// which the crate takes when the inputs are not finite (tensor.rs:197-201):
+//   y = dot_scores(x_r, w_n) + (bias[n] or 0.0)     w_n dequantized (dequant)
+//   y = y + scale * (dot_scores(mid_r, B_n) + 0.0)   with an adapter (Adapter::combine)
+// stored through the epilogue.  The dot products run in dot_scores' order, so
+// NaN and infinity propagate as in the crate.  A block computes 32 rows x 64
+// columns; thread (tr, tc) owns rows 2tr, 2tr+1 and columns tc + 16j (j < 4)
+// with eight lane sums each.  Per group of 64 inputs the block stages x and
+// the dequantized weights in LDS (rows padded to 68 floats: the 16 columns a
+// wave reads per step fall in distinct banks).
+constexpr int kF32Rows = 32, kF32Cols = 64, kF32Pad = 68;
+__global__ __launch_bounds__(256) void k_linear_fp32(FProj P) {
+  __shared__ __attribute__((aligned(16))) float xs[kF32Rows][kF32Pad];
+  __shared__ __attribute__((aligned(16))) float ws[kF32Cols][kF32Pad];
+  if (P.when && *P.when == 0) return;  // the inputs were finite: the int8 kernels ran
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+  const int col_tiles = (P.n + kF32Cols - 1) / kF32Cols;
+  const int m0 = (int)(blockIdx.x / col_tiles) * kF32Rows, n0 = (int)(blockIdx.x % col_tiles) * kF32Cols;
+  const int chunks = P.k >> 3;  // full chunks of 8 go to the lane sums
+  float acc[2][4][8];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc[i][j][q] = 0.0f;
+  for (int g = 0; 8 * g < chunks; ++g) {
+    const int nfull = min(8, chunks - 8 * g);  // uniform over the block
+    __syncthreads();                           // the previous group's reads are done
+    {
+      // x: thread t stages row t/8, inputs 64g + 8(t%8) .. +8 (zero past m or k)
+      const int r = tid >> 3, seg = tid & 7, row = m0 + r, kk = 64 * g + 8 * seg;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        xs[r][8 * seg + u] = (row < P.m && kk + u < P.k) ? P.x[(size_t)row * P.k + kk + u] : 0.0f;
+    }
+    {
+      // w: thread t stages column t/4, 16 inputs from one fragment lane (the
+      // repacked layout is zero past n and k, and n0 + 63 < np)
+      const int c = tid >> 2, h = (tid >> 1) & 1, part = tid & 1, n = n0 + c;
+      const uint4 raw = *reinterpret_cast<const uint4*>(
+          P.wt + ((size_t)((n >> 5) * P.g + g) * 2 + h) * kFragBytes + ((n & 31) + 32 * part) * 16);
+      const float sc = P.wst[(size_t)g * P.np + n];
+      const uint32_t word[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int u = 0; u < 16; ++u) ws[c][32 * h + 16 * part + u] = (float)(int8_t)(word[u >> 2] >> (8 * (u & 3))) * sc;
+    }
+    __syncthreads();
+    for (int cc = 0; cc < nfull; ++cc) {
+      float xv[2][8], wv[4][8];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float4 a = *reinterpret_cast<const float4*>(&xs[2 * tr + i][8 * cc]);
+        const float4 b = *reinterpret_cast<const float4*>(&xs[2 * tr + i][8 * cc + 4]);
+        xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
+        xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 a = *reinterpret_cast<const float4*>(&ws[tc + 16 * j][8 * cc]);
+        const float4 b = *reinterpret_cast<const float4*>(&ws[tc + 16 * j][8 * cc + 4]);
+        wv[j][0] = a.x; wv[j][1] = a.y; wv[j][2] = a.z; wv[j][3] = a.w;
+        wv[j][4] = b.x; wv[j][5] = b.y; wv[j][6] = b.z; wv[j][7] = b.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[i][j][q] = acc[i][j][q] + xv[i][q] * wv[j][q];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = m0 + 2 * tr + i;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = n0 + tc + 16 * j;
+      if (row >= P.m || n >= P.n) continue;
+      float y = -0.0f;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) y = y + acc[i][j][q];
+      for (int t = 8 * chunks; t < P.k; ++t) y = y + P.x[(size_t)row * P.k + t] * dequant(P, n, t);
+      y = y + (P.bias ? P.bias[n] : 0.0f);
+      if (P.lora) {
+        const float delta =
+            (P.rank > 0 ? dot_scores_rows(P.lmid + (size_t)row * P.rank, P.lb + (size_t)n * P.rank, P.rank) : -0.0f) +
+            0.0f;
+        const float scaled = P.lscale * delta;
+        y = y + scaled;
+      }
+      float* dst = P.layout == 1 ? P.out + (size_t)n * P.m + row : P.out + (size_t)row * P.n + n;
+      if (P.epilogue == 0 || P.layout == 1) *dst = y;
+      else if (P.epilogue == 1) *dst = *dst + y;
+      else *dst = silu(*dst) * y;
+    }
+  }
+}
+
 }  // namespace
 
 static unsigned blocks_for(long n, int per) { return (unsigned)((n + per - 1) / per); }
+
+__global__ void k_fill_u32(uint32_t* p, uint32_t v) { *p = v; }
+__global__ void k_or_u32(uint32_t* dst, const uint32_t* src) {
+  if (*src) atomicOr(dst, *src);
+}
+
+hipError_t launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t s) {
+  k_fill_u32<<<1, 1, 0, s>>>(p, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_or_u32(uint32_t* dst, const uint32_t* src, hipStream_t s) {
+  k_or_u32<<<1, 1, 0, s>>>(dst, src);
+  return hipGetLastError();
+}
+
+hipError_t launch_linear_fp32(const FProj& p, hipStream_t s) {
+  if (p.m == 0 || p.n == 0) return hipSuccess;
+  const long blocks = (long)((p.m + kF32Rows - 1) / kF32Rows) * ((p.n + kF32Cols - 1) / kF32Cols);
+  k_linear_fp32<<<(unsigned)blocks, 256, 0, s>>>(p);
+  return hipGetLastError();
+}
 
 hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int rank, float* mid, hipStream_t s) {
   const long waves = (long)((m + 3) / 4) * ((rank + 7) / 8);

@@ -119,6 +119,8 @@ def lib() -> ctypes.CDLL:
         "dq8_ffn": ([_vp, ctypes.POINTER(_FfnWeights), _vp, _vp, _sz, _vp, _vp, _vp, _vp], _i),
         "dq8_group_dots": ([_vp, _vp, _vp, _sz, _vp, _vp], _i),
         "dq8_status_string": ([_i], ctypes.c_char_p),
+        "dq8_linear_fp32": ([_vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
+        "dq8_apply": ([_vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
         "dq8_weights_from_raw": ([_vp, _vp, _i, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
         "dq8_weights_upload": ([_vp, _vp, _i, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
         "dq8_st_open": ([ctypes.c_char_p, ctypes.POINTER(_vp)], _i),
@@ -414,7 +416,9 @@ class Context:
     def ffn(self, gate: Weights, up: Weights, down: Weights, q, scales, residual, h=None, biases=(None, None, None),
             gate_lora: Lora | None = None, up_lora: Lora | None = None, down_lora=None, nonfinite=None):
         """One layer's FFN chain (qwen.rs:486-492): h = silu(gate(x)) * up(x); residual += down(h).
-        down_lora = (lora_A [rank][inter], lora_B [hidden][rank], scale) or None.  Returns h."""
+        down_lora = (lora_A [rank][inter], lora_B [hidden][rank], scale) or None.  Returns h.
+        A non-finite h sends down through the FP32 path, as in the crate; `nonfinite`
+        (a uint32 device scalar) then gets 1 ORed into it."""
         torch = _torch()
         self._dev(q, torch.int8, name="q")
         m, k = q.shape
@@ -456,6 +460,33 @@ class Context:
         _check(lib().dq8_linear_f32in(self.handle, w.handle, x.data_ptr(), m, _ptr(bias), out.data_ptr(), layout,
                                       epilogue, _stream(self.device)), "dq8_linear_f32in")
         return out
+
+    def _fp32_call(self, fn: str, w: Weights, x, out, bias, lora, layout, epilogue):
+        torch = _torch()
+        self._dev(x, torch.float32, name="x")
+        m, k = x.shape
+        if k != w.k:
+            raise Dq8Error(ERR_SHAPE, f"{fn}: input width differs from the weights")
+        shape = (m, w.n) if layout == ROWS else (w.n, m)
+        if out is None:
+            out = torch.zeros(shape, dtype=torch.float32, device=self.device)
+        self._dev(out, torch.float32, shape, "out")
+        if bias is not None:
+            self._dev(bias, torch.float32, (w.n,), "bias")
+        lo = self._lora(lora, m, w.n) if lora is not None else None
+        _check(getattr(lib(), fn)(self.handle, w.handle, x.data_ptr(), m, _ptr(bias),
+                                  ctypes.byref(lo) if lo is not None else None, out.data_ptr(), layout, epilogue,
+                                  _stream(self.device)), fn)
+        return out
+
+    def linear_fp32(self, w: Weights, x, out=None, bias=None, lora: Lora | None = None, layout=ROWS, epilogue=WRITE):
+        """Projection::columns_tiled: the FP32 path over dequantized weights."""
+        return self._fp32_call("dq8_linear_fp32", w, x, out, bias, lora, layout, epilogue)
+
+    def apply(self, w: Weights, x, out=None, bias=None, lora: Lora | None = None, layout=ROWS, epilogue=WRITE):
+        """Projection::apply_quantized on fp32 x: the int8 path, or the FP32 path
+        if x holds a non-finite value, chosen on the device."""
+        return self._fp32_call("dq8_apply", w, x, out, bias, lora, layout, epilogue)
 
     def linear_batch(self, items: list[Item]) -> None:
         torch = _torch()

@@ -182,14 +182,30 @@ typedef struct dq8_ffn_weights {
  *   residual += down(h)                  Add, h re-quantized per token (apply_into)
  * q/scales are the FFN input's quantization, shared by gate and up (the
  * SharedInput of qwen.rs:488).  h [m][inter] is written (the crate's `gate`
- * buffer) and quantized on the device for down.  If h holds a
- * non-finite value the crate's down projection takes its FP32 path: with
- * nonfinite == NULL this call synchronizes after up and returns
- * DQ8_ERR_NONFINITE with h written and residual untouched, for the caller's FP32
- * path; otherwise it ORs 1 into *nonfinite and runs down anyway (its result then
- * to be discarded by the caller). */
+ * buffer) and quantized on the device for down.  If h holds a non-finite
+ * value, the down projection takes the crate's FP32 path (tensor.rs:197-201,
+ * dq8_linear_fp32), chosen on the device: the call never synchronizes.  If
+ * nonfinite is not NULL, 1 is ORed into *nonfinite when that happened. */
 dq8_status dq8_ffn(dq8_ctx *ctx, const dq8_ffn_weights *f, const int8_t *q, const float *scales, size_t m, float *h,
                    float *residual, uint32_t *nonfinite, void *stream);
+/* Projection::columns_tiled (tensor.rs:206-269), the FP32 path that
+ * Projection::apply_quantized takes when QuantizedInputs::new(x) is None
+ * (tensor.rs:197-201): for fp32 x [m][k], every output is
+ *   y = dot_scores(x_r, w_n) + (bias[n] or 0.0),  w_n[t] = (float)q * scale
+ * (Data::row, weights.rs:47-78), in dot_scores' x86-64 order (tensor.rs:6-25),
+ * then the adapter term of Adapter::combine (lora may be NULL), stored through
+ * the epilogue.  NaN and infinity propagate as in the crate. */
+dq8_status dq8_linear_fp32(dq8_ctx *ctx, const dq8_weights *w, const float *x, size_t m, const float *bias,
+                           const dq8_lora *lora, float *out, dq8_layout layout, dq8_epilogue epilogue,
+                           void *stream);
+/* Projection::apply_quantized (tensor.rs:127-202) on fp32 inputs x [m][k]:
+ * quantize x (QuantizedInputs::new), then the int8 projection, or the FP32
+ * path of dq8_linear_fp32 if x holds a non-finite value.  Both are queued and
+ * a device flag lets exactly one run: no synchronization, the crate's result
+ * either way.  Uses the context workspace (calls of one context are ordered). */
+dq8_status dq8_apply(dq8_ctx *ctx, const dq8_weights *w, const float *x, size_t m, const float *bias,
+                     const dq8_lora *lora, float *out, dq8_layout layout, dq8_epilogue epilogue, void *stream);
+
 /* Several independent projections in one launch (same-shape inputs are not
  * required).  Each item is one dq8_linear (or dq8_linear_lora).  This is the shape of a model
  * layer's projections that read already-available inputs (q/k/v, GDN

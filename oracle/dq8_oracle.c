@@ -382,6 +382,59 @@ float dq8o_lora_combine(float base, const float *mid_row, const float *b_row, si
     return base + scaled;
 }
 
+int dq8o_linear_lora(const float *x, size_t rows, size_t width, const uint8_t *w, const float *ws, size_t outputs,
+                     const float *bias, const float *a, const float *b, size_t rank, float scale, float *result,
+                     int epilogue, int threads);
+/* Data::row of 8-bit Quantized data (weights.rs:47-78): element i of row r is
+ * (float)(int8)values[r][i] * scales[r][i / 64], one rounding. */
+void dq8o_dequantize_weights(const uint8_t *w, const float *ws, size_t n, size_t k, float *out) {
+    size_t g = div_ceil(k, GROUP);
+    for (size_t r = 0; r < n; ++r)
+        for (size_t i = 0; i < k; ++i) out[r * k + i] = (float)(int8_t)w[r * k + i] * ws[r * g + i / GROUP];
+}
+
+/* Projection::apply_quantized (tensor.rs:127-202) with its FP32 fallback: if
+ * QuantizedInputs::new(x) is None (a non-finite input), the columns are
+ * columns_tiled (tensor.rs:206-269) over the dequantized weights --
+ * dot_scores(x_r, w_n) + bias -- and the adapter (a != NULL) adds
+ * scale * (dot_scores(mid_r, b_n) + 0.0) with mid = linear(x, A); otherwise the
+ * int8 path of dq8o_linear_lora / dq8o_linear.  Stores through the epilogue.
+ * Returns 1 if the FP32 path ran, 0 if the int8 path did, 2 on allocation failure. */
+int dq8o_apply(const float *x, size_t rows, size_t width, const uint8_t *w, const float *ws, size_t outputs,
+               const float *bias, const float *a, const float *b, size_t rank, float scale, float *result,
+               int epilogue, int threads) {
+    if (rows == 0) return 0;
+    int st = a ? dq8o_linear_lora(x, rows, width, w, ws, outputs, bias, a, b, rank, scale, result, epilogue, threads)
+               : dq8o_linear(x, rows, width, w, ws, outputs, bias, result, epilogue, threads);
+    if (st != 1) return st;
+    size_t nv = rows * outputs, nm = rows * rank;
+    float *deq = (float *)malloc((outputs * width > 0 ? outputs * width : 1) * sizeof(float));
+    float *values = (float *)malloc((nv > 0 ? nv : 1) * sizeof(float));
+    float *mid = (float *)malloc((nm > 0 ? nm : 1) * sizeof(float));
+    float *delta = (float *)malloc((nv > 0 ? nv : 1) * sizeof(float));
+    int status = 2;
+    if (deq && values && mid && delta) {
+        dq8o_dequantize_weights(w, ws, outputs, width, deq);
+        dq8o_linear_f32(x, rows, width, deq, outputs, bias, values, threads);
+        if (a) {
+            dq8o_lora_mid(x, rows, width, a, rank, mid, threads);
+            dq8o_linear_f32(mid, rows, rank, b, outputs, NULL, delta, threads);
+            for (size_t i = 0; i < nv; ++i) {
+                float scaled = scale * delta[i];
+                values[i] = values[i] + scaled;
+            }
+        }
+        for (size_t i = 0; i < nv; ++i) {
+            if (epilogue == 0) result[i] = values[i];
+            else if (epilogue == 1) result[i] = result[i] + values[i];
+            else result[i] = dq8o_silu(result[i]) * values[i];
+        }
+        status = 1;
+    }
+    free(deq); free(values); free(mid); free(delta);
+    return status;
+}
+
 /* The x86 (non-SDOT) plan of Linear::apply_into_shared with a LoRA pair
  * (weights.rs:450-491): values = linear(x, W, bias) (the int8 projection);
  * mid = linear(x, A); delta = linear(mid, B); values[i] += scale * delta[i];

@@ -64,6 +64,11 @@ def lib():
         L.dq8o_linear_lora.argtypes = [_f32p, _sz, _sz, _u8p, _f32p, _sz, ctypes.c_void_p, _f32p, _f32p, _sz,
                                        ctypes.c_float, _f32p, ctypes.c_int, ctypes.c_int]
         L.dq8o_linear_lora.restype = ctypes.c_int
+        L.dq8o_dequantize_weights.argtypes = [_u8p, _f32p, _sz, _sz, _f32p]
+        L.dq8o_dequantize_weights.restype = None
+        L.dq8o_apply.argtypes = [_f32p, _sz, _sz, _u8p, _f32p, _sz, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_void_p, _sz, ctypes.c_float, _f32p, ctypes.c_int, ctypes.c_int]
+        L.dq8o_apply.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -281,3 +286,36 @@ def linear_lora(x, w, ws, a, b, scale: float, bias=None, result=None, epilogue: 
     if st != 0:
         raise MemoryError("oracle allocation failed")
     return out
+
+
+def dequantize_weights(w, ws) -> np.ndarray:
+    """Data::row of 8-bit Quantized weights: (float)q * scale, [N][K] float32."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    ws = np.ascontiguousarray(ws, dtype=np.float32)
+    n, k = w.shape
+    out = np.zeros((n, k), np.float32)
+    lib().dq8o_dequantize_weights(w, ws, n, k, out)
+    return out
+
+
+def apply(x, w, ws, bias=None, a=None, b=None, scale=0.0, result=None, epilogue: int = 0, threads: int = 1):
+    """Projection::apply_quantized with the FP32 fallback for non-finite x.
+    Returns (result [M][N], fp32_path_taken)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    ws = np.ascontiguousarray(ws, dtype=np.float32)
+    rows, width = x.shape
+    n = w.shape[0]
+    out = np.zeros((rows, n), np.float32) if result is None else np.array(result, dtype=np.float32, copy=True, order="C")
+    keep, bp = _bias_ptr(bias)
+    rank = 0
+    ap = bpp = None
+    if a is not None:
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        rank = a.shape[0]
+        ap, bpp = a.ctypes.data_as(ctypes.c_void_p), b.ctypes.data_as(ctypes.c_void_p)
+    st = lib().dq8o_apply(x, rows, width, w, ws, n, bp, ap, bpp, rank, scale, out, epilogue, threads)
+    if st == 2:
+        raise MemoryError("dq8o_apply")
+    return out, st == 1

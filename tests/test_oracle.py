@@ -596,3 +596,81 @@ def test_silu_n_matches_scalar_silu():
     want = np.array([dq8o.silu(float(v)) for v in x], np.float32)
     assert y.tobytes() == want.tobytes()
     assert dq8o.silu(0.0) == 0.0 and dq8o.silu(-200.0) == 0.0 and dq8o.silu(200.0) == 200.0
+
+
+# ------------------------------------------------------ FP32 fallback path
+# Projection::apply_quantized takes columns_tiled (tensor.rs:206-269) when
+# QuantizedInputs::new returns None: dot_scores over the dequantized weights
+# (Data::row, weights.rs:47-78).
+
+def test_dequantize_known_answers_and_bound():
+    w = np.array([[1, 255, 127, 129, 0, 128]], np.uint8)  # 1, -1, 127, -127, 0, -128
+    ws = np.array([[0.25]], np.float32)
+    assert dq8o.dequantize_weights(w, ws).tolist() == [[0.25, -0.25, 31.75, -31.75, 0.0, -32.0]]
+    rng = np.random.default_rng(17)
+    x = (rng.standard_normal((9, 200)) * 3).astype(np.float32)
+    v, s = dq8o.quantize_weights(x)
+    d = dq8o.dequantize_weights(v, s)
+    for g in range(4):
+        blk = slice(64 * g, min(64 * g + 64, 200))
+        assert np.all(np.abs(d[:, blk] - x[:, blk]) <= s[:, g:g + 1] / 2 * (1 + 1e-6))
+
+
+def _fallback_case(rng, rows, width, outputs, rank=0):
+    x = (rng.standard_normal((rows, width)) * 2).astype(np.float32)
+    v, s = dq8o.quantize_weights((rng.standard_normal((outputs, width)) * 0.1).astype(np.float32))
+    bias = rng.standard_normal(outputs).astype(np.float32)
+    a = b = None
+    if rank:
+        a = (rng.standard_normal((rank, width)) * 0.1).astype(np.float32)
+        b = (rng.standard_normal((outputs, rank)) * 0.1).astype(np.float32)
+    return x, v, s, bias, a, b
+
+
+@pytest.mark.parametrize("rank", [0, 3, 11])
+def test_fallback_outputs_are_dot_scores_of_dequantized_rows(rank):
+    rng = np.random.default_rng(rank + 5)
+    rows, width, outputs = 4, 75, 6
+    x, v, s, bias, a, b = _fallback_case(rng, rows, width, outputs, rank)
+    x[1, 30] = np.nan  # the whole projection takes the FP32 path (tensor.rs:318-320)
+    got, fp32 = dq8o.apply(x, v, s, bias=bias, a=a, b=b, scale=0.5)
+    assert fp32
+    d = dq8o.dequantize_weights(v, s)
+    for r in range(rows):
+        for n in range(outputs):
+            want = f32(py_dot_scores(x[r], d[n]) + float(bias[n]))
+            if rank:
+                mid = [f32(py_dot_scores(x[r], a[j]) + 0.0) for j in range(rank)]
+                delta = f32(py_dot_scores(mid, b[n]) + 0.0)
+                want = f32(want + f32(0.5 * delta))
+            if r == 1:
+                assert np.isnan(got[r, n])
+            else:
+                assert got[r, n] == np.float32(want), (r, n)
+
+
+def test_finite_inputs_take_the_int8_path_and_the_paths_differ():
+    rng = np.random.default_rng(8)
+    x, v, s, bias, _, _ = _fallback_case(rng, 5, 130, 7)
+    got, fp32 = dq8o.apply(x, v, s, bias=bias)
+    assert not fp32
+    assert got.tobytes() == dq8o.linear(x, v, s, bias=bias).tobytes()
+    # the FP32 path on the same finite input gives different bits, so a device
+    # result from the wrong path cannot pass a bitwise check
+    d = dq8o.dequantize_weights(v, s)
+    fp = np.array([[py_dot_scores(x[r], d[n]) + float(bias[n]) for n in range(7)] for r in range(5)], np.float32)
+    assert fp.tobytes() != got.tobytes()
+
+
+def test_fallback_epilogues_store_like_write_columns():
+    rng = np.random.default_rng(9)
+    x, v, s, bias, _, _ = _fallback_case(rng, 3, 64, 5)
+    x[2, 0] = np.inf
+    base = rng.standard_normal((3, 5)).astype(np.float32)
+    w, _ = dq8o.apply(x, v, s, bias=bias)
+    add, _ = dq8o.apply(x, v, s, bias=bias, result=base, epilogue=1)
+    sw, _ = dq8o.apply(x, v, s, bias=bias, result=base, epilogue=2)
+    with np.errstate(invalid="ignore"):
+        assert np.array_equal(add, (base + w).astype(np.float32), equal_nan=True)
+    want = np.array([dq8o.silu(o) * e for o, e in zip(base.ravel(), w.ravel())], np.float32).reshape(3, 5)
+    assert np.array_equal(sw, want, equal_nan=True)
