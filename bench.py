@@ -267,6 +267,7 @@ def main():
     torch.cuda.empty_cache()
 
     stacked, skinny = run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen)
+    load = run_load(args, torch, dq8, ctx, gen)
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, torch, dq8, ctx, dev, gen)
     traffic = load_traffic("linear_wide_stack2048")
     out = {
@@ -306,6 +307,7 @@ def main():
         },
         "skinny": skinny,
         "questions_stacked": stacked,
+        "load": load,
         "lora": lora,
         "cpu_baseline": cpu,
     }
@@ -480,6 +482,54 @@ def run_stacked(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, wb
         "tops": round(ops / (ms * 1e-3) / 1e12, 1),
         "weight_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
         "speedup_vs_per_question_launches": round(per_question_ms / (ms / args.questions), 2),
+    }
+
+
+def run_load(args, torch, dq8, ctx, gen):
+    """Weight load path: one layer set's projections (the skinny leg's shapes) as
+    BF16 tensors of one safetensors file, read by dq8_st_load_weights into
+    quantized, repacked device weights (file -> pinned staging -> device decode,
+    check, quantize, repack).  The file is written first, so it is read from
+    the page cache: this is the host-memory-to-weights rate, not a disk rate."""
+    import json as _json
+    import struct as _struct
+    import tempfile
+
+    shapes = [("q", HIDDEN, HIDDEN), ("k", 512, HIDDEN), ("v", 512, HIDDEN), ("o", HIDDEN, HIDDEN),
+              ("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN), ("gate", FFN_DIM, HIDDEN),
+              ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
+    header, blobs, off = {}, [], 0
+    for name, n, k in shapes:
+        t = (torch.randn((n, k), generator=gen, device="cuda") * 0.02).to(torch.bfloat16).cpu()
+        b = t.view(torch.int16).numpy().tobytes()
+        header[f"layers.0.{name}_proj.weight"] = {"dtype": "BF16", "shape": [n, k], "data_offsets": [off, off + len(b)]}
+        blobs.append(b)
+        off += len(b)
+    text = _json.dumps(header).encode()
+    fd, path = tempfile.mkstemp(suffix=".safetensors")
+    try:
+        with os.fdopen(fd, "wb") as f:
+            f.write(_struct.pack("<Q", len(text)) + text + b"".join(blobs))
+        del blobs
+        times = []
+        for _ in range(3):
+            with dq8.SafeTensors(path) as st:
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                ws = [st.load_weights(ctx, name) for name in st.names]
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+                for w in ws:
+                    w.free()
+    finally:
+        os.unlink(path)
+    best = min(times)
+    return {
+        "workload": "one layer set's 9 projection weights (q,k,v,o, GDN in/out, FFN gate/up/down) as BF16 in one "
+                    "safetensors file (page cache) -> quantized device weights",
+        "file_bytes": off,
+        "ms": round(best * 1e3, 2),
+        "gbs": round(off / best / 1e9, 2),
     }
 
 
