@@ -52,6 +52,7 @@ def parse():
     p.add_argument("--weight-copies", type=int, default=5)
     p.add_argument("--skinny-reps", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-graph", action="store_true", help="time eager submission only (no HIP graph replay)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--lora-rank", type=int, default=16,
                    help="rank of the LoRA adapters of the stack's second pass (0: skip it)")
@@ -88,7 +89,9 @@ def main():
         return
     ctx = dq8.Context(0)
     lib = dq8.lib()
-    stream = torch.cuda.current_stream(dev)
+    # all work on one side stream (default priority): it can be graph-captured
+    stream = torch.cuda.Stream(dev)
+    torch.cuda.set_stream(stream)
     sh = stream.cuda_stream
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
@@ -227,22 +230,43 @@ def main():
     torch.cuda.synchronize()
     if int(flag.item()) != 0:
         raise RuntimeError("synthetic activations were reported non-finite")
-    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in calls]
-          for _ in range(args.steps)]
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for s in range(args.steps):
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / args.steps
+
+    # eager: every call submitted from the host in turn
+    ms_eager = timed(run_step)
+    # graph: the same calls captured once and replayed (no per-launch host work)
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            run_step()
+        for _ in range(args.warmup):
+            graph.replay()
+        ms_graph = timed(graph.replay)
+    ms_step = ms_graph if graph is not None else ms_eager
+    # per-launch durations: HIP events around each call, on the launch stream,
+    # over as many eager steps again (events in the timed steps would slow the
+    # host's submission and add gaps to the step time)
+    ev_steps = args.steps
+    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in calls]
+          for _ in range(ev_steps)]
+    for s in range(ev_steps):
         run_step(ev[s])
-    t1.record(stream)
     torch.cuda.synchronize()
-    ms_total = t0.elapsed_time(t1)
-    ms_step = ms_total / args.steps
     lin_ms = quant_ms = 0.0
     lin_n = quant_n = 0
     quant_bytes = sum(c[3][0] for c in calls if c[0] == "quant")
-    for s in range(args.steps):
+    for s in range(ev_steps):
         for i, c in enumerate(calls):
             d = ev[s][i][0].elapsed_time(ev[s][i][1])
             if c[0] == "linear":
@@ -290,9 +314,11 @@ def main():
             "hidden": HIDDEN,
             "ops_per_step": step_ops,
             "frac_of_int8_peak": round(value / PEAK_INT8_TOPS, 4),
-            "quantize_ms_per_step": round(quant_ms / args.steps, 4),
-            "quantize_gbs": round(quant_bytes * args.steps / (quant_ms * 1e-3) / 1e9, 1),
-            "projection_ms_per_step": round(lin_ms / args.steps, 4),
+            "submission": "hip graph replay of the captured step" if graph is not None else "eager",
+            "eager_ms_per_step": round(ms_eager, 4),
+            "quantize_ms_per_step": round(quant_ms / ev_steps, 4),
+            "quantize_gbs": round(quant_bytes * ev_steps / (quant_ms * 1e-3) / 1e9, 1),
+            "projection_ms_per_step": round(lin_ms / ev_steps, 4),
         },
         "roofline": {
             "kernel": "k_linear_wide",
@@ -322,19 +348,33 @@ def run_lora_stack(args, torch, stream, build, run_step, step_ops, base_ms):
     for _ in range(2):
         run_step(calls=calls)
     torch.cuda.synchronize()
-    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in calls]
-          for _ in range(args.steps)]
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # submitted the same way as the base step it is compared with
+    step = lambda: run_step(calls=calls)
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            run_step(calls=calls)
+        graph.replay()
+        step = graph.replay
+    torch.cuda.synchronize()
     t0.record(stream)
-    for s in range(args.steps):
-        run_step(ev[s], calls=calls)
+    for _ in range(args.steps):
+        step()
     t1.record(stream)
     torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / args.steps
-    mid_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(args.steps)
-                 for i, c in enumerate(calls) if c[0] == "mid") / args.steps
-    lin_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(args.steps)
-                 for i, c in enumerate(calls) if c[0] == "linear") / args.steps
+    ev_steps = 3
+    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in calls]
+          for _ in range(ev_steps)]
+    for s in range(ev_steps):
+        run_step(ev[s], calls=calls)
+    torch.cuda.synchronize()
+    mid_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(ev_steps)
+                 for i, c in enumerate(calls) if c[0] == "mid") / ev_steps
+    lin_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(ev_steps)
+                 for i, c in enumerate(calls) if c[0] == "linear") / ev_steps
     return {
         "workload": f"the stack above with a rank-{args.lora_rank} FP32 LoRA pair on every projection",
         "rank": args.lora_rank,
