@@ -222,58 +222,79 @@ __device__ __forceinline__ void decode4(const void* base, size_t i, float (&v)[4
 // rounds half away from zero, as f32::round.  x holds DT elements; a
 // non-finite one ORs 1 into *nonfinite (Data::read rejects it for weights,
 // QuantizedInputs::new returns None for inputs).
-template <int DT>
+template <int DT, int PER>
 __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, int rows, int k, int8_t* __restrict__ q,
                                                   int ldq, float* __restrict__ scales, int lds, uint32_t* nonfinite) {
   constexpr int ES = DT == kDtypeF32 ? 4 : 2;  // element bytes
   const int lane = threadIdx.x & 63;
   const int chunks = (k + 255) >> 8;
-  const long item = (long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  if (item >= (long)rows * chunks) return;
-  const int row = (int)(item / chunks);
-  const int chunk = (int)(item - (long)row * chunks);
-  const int k0 = chunk * 256 + lane * 4;
-  const size_t r0 = (size_t)row * k;
-  float v[4];
-  if ((k & 3) == 0 && k0 + 3 < k && ((uintptr_t)x & (4 * ES - 1)) == 0) {
-    decode4<DT>(x, r0 + k0, v);
-  } else {
+  const long total = (long)rows * chunks;
+  // PER consecutive 256-element chunks per wave, all loaded before any is used
+  const long first = ((long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * PER;
+  if (first >= total) return;  // wave-uniform
+  const bool vec = (k & 3) == 0 && ((uintptr_t)x & (4 * ES - 1)) == 0;
+  float v[PER][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = (k0 + i < k) ? decode<DT>(x, r0 + k0 + i) : 0.0f;
-  }
-  bool bad = false;
-  float m = 0.0f;
+  for (int p = 0; p < PER; ++p) {
+    const long item = min(first + p, total - 1);  // past the end: recomputes the last chunk, not stored
+    const int row = (int)(item / chunks), chunk = (int)(item - (long)row * chunks);
+    const int k0 = chunk * 256 + lane * 4;
+    const size_t r0 = (size_t)row * k;
+    if (vec && k0 + 3 < k) {
+      decode4<DT>(x, r0 + k0, v[p]);
+    } else {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    bad |= !isfinite(v[i]);
-    m = fmaxf(m, fabsf(v[i]));
+      for (int i = 0; i < 4; ++i) v[p][i] = (k0 + i < k) ? decode<DT>(x, r0 + k0 + i) : 0.0f;
+    }
   }
-  if (bad && nonfinite) atomicOr(nonfinite, 1u);
-  // max over the 16 lanes of this group (fmaxf of non-negative values is order-free)
-  m = fmaxf(m, __shfl_xor(m, 1));
-  m = fmaxf(m, __shfl_xor(m, 2));
-  m = fmaxf(m, __shfl_xor(m, 4));
-  m = fmaxf(m, __shfl_xor(m, 8));
-  const float scale = (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
-  uint32_t packed = 0;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float r = roundf(v[i] / scale);
-    r = fminf(fmaxf(r, -127.0f), 127.0f);
-    packed |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * i);
-  }
-  int8_t* qr = q + (size_t)row * ldq;
-  if ((ldq & 3) == 0 && k0 + 3 < ldq && ((uintptr_t)q & 3) == 0) {
-    // Padding bytes [k, ldq) are written as zero (v = 0 there).
-    *reinterpret_cast<uint32_t*>(qr + k0) = packed;
-  } else {
+  for (int p = 0; p < PER; ++p) {
+    const long item = first + p;
+    if (item >= total) break;  // wave-uniform
+    const int row = (int)(item / chunks), chunk = (int)(item - (long)row * chunks);
+    const int k0 = chunk * 256 + lane * 4;
+    bool bad = false;
+    float m = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (k0 + i < ldq) qr[k0 + i] = (int8_t)(packed >> (8 * i));
+    for (int i = 0; i < 4; ++i) {
+      bad |= !isfinite(v[p][i]);
+      m = fmaxf(m, fabsf(v[p][i]));
+    }
+    if (bad && nonfinite) atomicOr(nonfinite, 1u);
+    // max over the 16 lanes of this group (fmaxf of non-negative values is order-free)
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    m = fmaxf(m, __shfl_xor(m, 4));
+    m = fmaxf(m, __shfl_xor(m, 8));
+    const float scale = (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
+    // round(v / scale) with the IEEE quotient, through a reciprocal: a = v *
+    // rcp(scale) is within 2 ulp of v / scale, so rounding a half away from
+    // zero gives the same integer unless a lies within 2^-15 (>= 4 ulp, as
+    // |a| < 128) of a half-integer; those rare elements divide exactly.
+    const float rs = __builtin_amdgcn_rcpf(scale);
+    uint32_t packed = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a = v[p][i] * rs;
+      const float fa = fabsf(a);
+      float r = roundf(a);
+      if (!(fabsf(fa - floorf(fa) - 0.5f) > 0x1p-15f)) r = roundf(v[p][i] / scale);
+      r = fminf(fmaxf(r, -127.0f), 127.0f);
+      packed |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * i);
+    }
+    int8_t* qr = q + (size_t)row * ldq;
+    if ((ldq & 3) == 0 && k0 + 3 < ldq && ((uintptr_t)q & 3) == 0) {
+      // Padding bytes [k, ldq) are written as zero (v = 0 there).
+      *reinterpret_cast<uint32_t*>(qr + k0) = packed;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (k0 + i < ldq) qr[k0 + i] = (int8_t)(packed >> (8 * i));
+    }
+    const int group = (chunk * 256 + (lane & ~15) * 4) / kGroup;
+    const int groups = (k + kGroup - 1) / kGroup;
+    if ((lane & 15) == 0 && group < groups) scales[(size_t)row * lds + group] = scale;
   }
-  const int group = (chunk * 256 + (lane & ~15) * 4) / kGroup;
-  const int groups = (k + kGroup - 1) / kGroup;
-  if ((lane & 15) == 0 && group < groups) scales[(size_t)row * lds + group] = scale;
 }
 
 // Reference layout -> fragment layout (see Weights in dq8_internal.h).
@@ -425,6 +446,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 #endif
 #ifndef DQ8_WIDE_WPE
 #define DQ8_WIDE_WPE 0
+#endif
+// 256-element chunks per wave of the quantizer.
+#ifndef DQ8_QUANT_PER
+#define DQ8_QUANT_PER 1
 #endif
 // Launches of at most this many blocks (three times as many when they mix
 // long and short K) use a ring of STAGES + 1 groups.
@@ -1406,12 +1431,16 @@ hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int ran
 
 hipError_t launch_quantize_raw(const void* x, int dtype, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
                                uint32_t* nonfinite, hipStream_t s) {
-  const long waves = (long)rows * ((k + 255) / 256);
-  if (waves == 0) return hipSuccess;
-  const int blocks = blocks_for(waves, 4);
-  if (dtype == kDtypeBF16) k_quantize<kDtypeBF16><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
-  else if (dtype == kDtypeF16) k_quantize<kDtypeF16><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
-  else k_quantize<kDtypeF32><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
+  constexpr int PER = DQ8_QUANT_PER;
+  const long items = (long)rows * ((k + 255) / 256);
+  if (items == 0) return hipSuccess;
+  const int blocks = blocks_for(blocks_for(items, PER), 4);
+  if (dtype == kDtypeBF16)
+    k_quantize<kDtypeBF16, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
+  else if (dtype == kDtypeF16)
+    k_quantize<kDtypeF16, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
+  else
+    k_quantize<kDtypeF32, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
   return hipGetLastError();
 }
 

@@ -72,6 +72,26 @@ def test_quantize_bit_exact(ctx, rows, width, kind):
     assert bits_equal(host(s), want_s)
 
 
+def test_quantize_values_next_to_half_integer_boundaries(ctx):
+    # Every element of a group is (k + 0.5) * scale, rounded, and moved by up
+    # to 2 ulp either way, for random k in -127..126: the quotient by the scale
+    # lands on or next to a rounding boundary, where an approximate quotient
+    # could round the other way.  Element 0 of each group sets the scale.
+    rng = np.random.default_rng(55)
+    rows = []
+    for _ in range(64):
+        m = np.float32(rng.uniform(0.1, 100.0) * 2.0 ** int(rng.integers(-20, 20)))
+        scale = np.float32(m / np.float32(127.0))
+        ks = rng.integers(-127, 127, size=63)
+        base = ((ks + 0.5) * np.float64(scale)).astype(np.float32)
+        vals = (base.view(np.int32) + rng.integers(-2, 3, size=63).astype(np.int32)).view(np.float32)
+        rows.append(np.concatenate([[m], np.clip(vals, -m, m)]).astype(np.float32))
+    x = np.stack(rows).reshape(16, 256)
+    q, s = ctx.quantize(dev(x))
+    qh, sh = dq8o.quantize_inputs(x)
+    assert np.array_equal(host(q), qh) and bits_equal(host(s), sh)
+
+
 @pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
 def test_quantize_nonfinite_is_reported(ctx, bad):
     x = np.ones((3, 70), np.float32)
