@@ -630,3 +630,27 @@ def test_ffn_chain_matches_the_reference_sequence(ctx, m, hidden, inter, lora):
         want_r = dq8o.linear(want_h, dv, ds, result=resid0, epilogue=1, threads=8)
     assert bits_equal(h, want_h)
     assert bits_equal(host(resid), want_r)
+
+
+def test_full_size_gdn_in_projection_properties(ctx):
+    # The headline stack's largest projection at full size (2048 tokens x
+    # 2048 -> 8224, 2112 wide blocks).  The oracle checks 64 sampled rows; the
+    # rest is pinned by properties that hold bit for bit: rows are independent
+    # (a row permutation of x permutes the result), and output columns are
+    # independent (the weights split in two launches give the same columns).
+    rng = np.random.default_rng(8224)
+    m, k, n = 2048, 2048, 8224
+    x = make_x(rng, m, k, "outliers")
+    wv, ws = dq8o.quantize_weights(make_w(rng, n, k))
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    full = host(ctx.linear(h, q, s))
+    rows = rng.choice(m, size=64, replace=False)
+    assert bits_equal(full[rows], dq8o.linear(x[rows], wv, ws, threads=8))
+    perm = rng.permutation(m)
+    qp, sp = ctx.quantize(dev(x[perm]))
+    assert bits_equal(host(ctx.linear(h, qp, sp)), full[perm])
+    cut = 3000
+    h1 = ctx.weights_from_quantized(dev(wv[:cut]), dev(ws[:cut]))
+    h2 = ctx.weights_from_quantized(dev(wv[cut:]), dev(ws[cut:]))
+    assert bits_equal(np.concatenate([host(ctx.linear(h1, q, s)), host(ctx.linear(h2, q, s))], axis=1), full)
