@@ -680,8 +680,8 @@ dq8_status dq8_lora_mid(dq8_ctx* ctx, const float* x, size_t m, size_t k, const 
   if (m == 0 || rank == 0) return DQ8_OK;
   if (!x || !a || !mid) return DQ8_ERR_ARG;
   if (k == 0 || m > (1u << 30) || k > (1u << 30) || rank > (1u << 20) || m * k > ((size_t)1 << 40) ||
-      rank * k > ((size_t)1 << 40))
-    return DQ8_ERR_SHAPE;
+      rank * k > ((size_t)1 << 40) || ((m + 7) / 8) * ((rank + 15) / 16) >= ((size_t)1 << 23))
+    return DQ8_ERR_SHAPE;  // the last bound keeps the grid under 2^32 work-items
   DeviceGuard guard(ctx->device);
   return from_hip(dq8::launch_lora_mid(x, (int)m, (int)k, a, (int)rank, mid, (hipStream_t)stream));
 }

@@ -1194,10 +1194,15 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
 }
 // LoRA middle product (weights.rs:480, 495): mid[r][j] = dot_scores(x_r, a_j)
 // + 0.0 for x [m][k], a [rank][k], in dot_scores' x86-64 order (tensor.rs:6-25).
+// Two kernels compute it in that order.  k_lora_mid_rows reads plain memory and
+// takes any shape and alignment; k_lora_mid_dma (below) stages tiles through
+// LDS and needs 16-byte aligned rows.
+//
+// k_lora_mid_rows:
 // A wave covers 4 rows and 8 columns j: lane l works on column j0 + l/8 and
 // holds lane i = l%8 of its partial sums (elements i, i+8, ...) for the 4 rows.
 // The 8 partial sums are then added in order, the tail elements one by one.
-__global__ __launch_bounds__(256) void k_lora_mid(const float* __restrict__ x, int m, int k, const float* __restrict__ a,
+__global__ __launch_bounds__(256) void k_lora_mid_rows(const float* __restrict__ x, int m, int k, const float* __restrict__ a,
                                                   int rank, float* __restrict__ mid) {
   const int lane = threadIdx.x & 63;
   const long wave = (long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1268,6 +1273,124 @@ __global__ __launch_bounds__(256) void k_lora_mid(const float* __restrict__ x, i
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       if (r0 + r < m) mid[(size_t)(r0 + r) * rank + j] = sum[r] + 0.0f;
+  }
+}
+
+// k_lora_mid_dma: a block of 4 waves covers 8 rows of x and 16 adapter rows.
+// Tiles of 256 inputs (8 x rows and 16 A rows, 1 KB each) reach LDS by direct
+// global->LDS loads in a ring of kMidSlots tiles, kMidSlots - 1 of them in
+// flight; wave w loads x rows 2w, 2w+1 and A rows 4w..4w+3 of every tile.
+// The products come from v_mfma_f32_4x4x1_16b_f32 with C = +0.0: each output
+// is one product rounded once, as a multiply (a zero product may lose its
+// sign, which no lane sum can see: a lane sum starts at +0.0, so it is never
+// -0.0, and s + 0.0 == s + -0.0 for every other s).  The VALU only adds.
+// Block b = 8g + i of the instruction holds lane sum i of rows 4g..4g+3 and
+// adapter rows 4w..4w+3 of this wave: A lane l = x[4(l/32) + l%4][8c + (l/4)%8],
+// B lane l = A[4w + l%4][8c + (l/4)%8], and output register r of lane l is the
+// product for row 4(l/32) + r, adapter row 4w + l%4, lane sum (l/4)%8.  The 8
+// lane sums of (row, adapter row) then sit in lanes (l & 32) + 4i + (l & 3);
+// they are added in order from -0.0, then the tail elements one by one.
+// Loads past the full chunks of 8 are clamped to the row's last 16 bytes and
+// never summed.  The row stride of 264 floats keeps the 32 distinct A inputs a
+// wave reads per chunk in distinct banks.
+// Requires k % 4 == 0 and 16-byte aligned x and a.
+constexpr int kMidRows = 8, kMidJ = 16, kMidKT = 256, kMidStride = kMidKT + 8;
+#ifndef DQ8_MID_SLOTS
+#define DQ8_MID_SLOTS 3
+#endif
+#ifndef DQ8_MID_BATCH
+#define DQ8_MID_BATCH 8
+#endif
+constexpr int kMidSlots = DQ8_MID_SLOTS, kMidLoads = 6;  // DMA loads per wave per tile
+constexpr int kMidBatch = DQ8_MID_BATCH;
+__global__ __launch_bounds__(256) void k_lora_mid_dma(const float* __restrict__ x, int m, int k,
+                                                      const float* __restrict__ a, int rank, float* __restrict__ mid) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) float lds[kMidSlots][kMidRows + kMidJ][kMidStride];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int jblocks = (rank + kMidJ - 1) / kMidJ;
+  const int r0 = (int)(blockIdx.x / jblocks) * kMidRows, j0 = (int)(blockIdx.x % jblocks) * kMidJ;
+  const int chunks = k >> 3, full = 8 * chunks;
+  const int tiles = (full + kMidKT - 1) / kMidKT;
+  const float* xrow[2];
+  const float* arow[4];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) xrow[q] = x + (size_t)min(r0 + 2 * w + q, m - 1) * k;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) arow[q] = a + (size_t)min(j0 + 4 * w + q, rank - 1) * k;
+  auto issue = [&](int t) {
+    const int kb = t * kMidKT;  // kb <= full - 8 <= k - 8
+    const uint32_t off = 4u * (uint32_t)min(4 * lane, k - 4 - kb);
+    float(*slot)[kMidStride] = lds[t % kMidSlots];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) dma16s(xrow[q] + kb, off, slot[2 * w + q]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) dma16s(arow[q] + kb, off, slot[kMidRows + 4 * w + q]);
+  };
+  const int i = (lane >> 2) & 7;
+  const int xr = 4 * (lane >> 5) + (lane & 3), jl = 4 * w + (lane & 3);
+  const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < kMidSlots - 1; ++t)
+    if (t < tiles) issue(t);
+  for (int t = 0; t < tiles; ++t) {
+    // this wave's loads of tile t are done once at most the newer tiles' remain
+    if (t + kMidSlots - 2 < tiles)
+      wait_vmcnt<(kMidSlots - 2) * kMidLoads>();
+    else
+      wait_vmcnt<0>();
+    lds_barrier();  // every wave's tile t has landed and tile t-1 is summed
+    if (t + kMidSlots - 1 < tiles) issue(t + kMidSlots - 1);  // the slot of tile t-1
+    const float* xs = lds[t % kMidSlots][xr] + i;
+    const float* as = lds[t % kMidSlots][kMidRows + jl] + i;
+    const int cmax = min(kMidKT / 8, chunks - t * (kMidKT / 8));
+    if (cmax == kMidKT / 8) {
+      // a full tile in batches of kMidBatch chunks: the products of the next
+      // batch are formed while the current batch is added
+      constexpr int NB = kMidKT / 8 / kMidBatch;
+      f32x4 d[2][kMidBatch];
+      auto products = [&](f32x4(&o)[kMidBatch], int c0) {
+        float xo[kMidBatch], ao[kMidBatch];
+#pragma unroll
+        for (int u = 0; u < kMidBatch; ++u) {
+          xo[u] = xs[8 * (c0 + u)];
+          ao[u] = as[8 * (c0 + u)];
+        }
+#pragma unroll
+        for (int u = 0; u < kMidBatch; ++u) o[u] = __builtin_amdgcn_mfma_f32_4x4x1f32(xo[u], ao[u], zero, 0, 0, 0);
+      };
+      products(d[0], 0);
+#pragma unroll
+      for (int bt = 0; bt < NB; ++bt) {
+        if (bt + 1 < NB) products(d[(bt + 1) & 1], kMidBatch * (bt + 1));
+#pragma unroll
+        for (int u = 0; u < kMidBatch; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = acc[r] + d[bt & 1][u][r];
+      }
+    } else {
+      for (int c = 0; c < cmax; ++c) {
+        const f32x4 d = __builtin_amdgcn_mfma_f32_4x4x1f32(xs[8 * c], as[8 * c], zero, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] = acc[r] + d[r];
+      }
+    }
+  }
+  const int j = j0 + jl;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float sum = -0.0f;
+#pragma unroll
+    for (int ii = 0; ii < 8; ++ii) sum = sum + __shfl(acc[r], (lane & 32) + 4 * ii + (lane & 3));
+    const int row = r0 + 4 * (lane >> 5) + r;
+    if (i == 0 && row < m && j < rank) {
+      const float* xg = x + (size_t)row * k;
+      const float* ag = a + (size_t)j * k;
+      for (int e = full; e < k; ++e) sum = sum + xg[e] * ag[e];
+      mid[(size_t)row * rank + j] = sum + 0.0f;
+    }
   }
 }
 
@@ -1422,9 +1545,14 @@ hipError_t launch_linear_fp32(const FProj& p, hipStream_t s) {
 }
 
 hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int rank, float* mid, hipStream_t s) {
-  const long waves = (long)((m + 3) / 4) * ((rank + 7) / 8);
-  if (waves == 0) return hipSuccess;
-  k_lora_mid<<<blocks_for(waves, 4), 256, 0, s>>>(x, m, k, a, rank, mid);
+  if (m == 0 || rank == 0) return hipSuccess;
+  if (k % 4 == 0 && ((size_t)x & 15) == 0 && ((size_t)a & 15) == 0) {
+    const long blocks = (long)((m + kMidRows - 1) / kMidRows) * ((rank + kMidJ - 1) / kMidJ);
+    k_lora_mid_dma<<<(unsigned)blocks, 256, 0, s>>>(x, m, k, a, rank, mid);
+  } else {
+    const long waves = (long)((m + 3) / 4) * ((rank + 7) / 8);
+    k_lora_mid_rows<<<blocks_for(waves, 4), 256, 0, s>>>(x, m, k, a, rank, mid);
+  }
   return hipGetLastError();
 }
 

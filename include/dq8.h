@@ -145,7 +145,9 @@ typedef struct dq8_lora {
 /* LoRA middle product (Linear::apply_into_shared, weights.rs:480 and 495):
  * mid [m][rank] = linear(x, A) with x fp32 [m][k] and A = lora_A fp32 [rank][k],
  * i.e. mid[r][j] = dot_scores(x_r, A_j) + 0.0 (the FP32 columns of
- * tensor.rs:206-269 without bias).  Non-finite inputs propagate as in the crate. */
+ * tensor.rs:206-269 without bias).  Non-finite inputs propagate as in the crate.
+ * DQ8_ERR_SHAPE for k == 0, m > 2^30, k > 2^30, rank > 2^20, m*k or rank*k
+ * above 2^40, or ceil(m/8) * ceil(rank/16) >= 2^23. */
 dq8_status dq8_lora_mid(dq8_ctx *ctx, const float *x, size_t m, size_t k, const float *a, size_t rank, float *mid,
                         void *stream);
 /* dq8_linear with the projection's LoRA adapter (Projection::apply_quantized with

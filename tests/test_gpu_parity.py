@@ -425,7 +425,13 @@ def test_config1_single_linear_seed0_bit_exact(ctx):
 
 # ------------------------------------------------------------------- LoRA
 
-LORA_MID_SHAPES = [(1, 64, 1), (5, 131, 13), (24, 2048, 16), (67, 100, 3), (130, 2048, 16), (9, 7, 9), (4, 6144, 8)]
+# The LDS-staged kernel takes k % 4 == 0 with 16-byte aligned rows; other
+# shapes take the plain-memory kernel.  Shapes cover ranks past one block of 16
+# adapter rows (full and partial), partial tiles of 256 inputs, k % 8 == 4
+# over several tiles, k with no full chunk of 8 (tail only) and full size.
+LORA_MID_SHAPES = [(1, 64, 1), (5, 131, 13), (24, 2048, 16), (67, 100, 3), (130, 2048, 16), (9, 7, 9), (4, 6144, 8),
+                   (130, 2048, 40), (9, 256, 64), (300, 1000, 24), (16, 8, 17), (33, 4, 5), (8, 2052, 16),
+                   (2048, 2048, 16), (17, 264, 33)]
 
 
 @pytest.mark.parametrize("m,k,rank", LORA_MID_SHAPES)
@@ -435,6 +441,59 @@ def test_lora_mid_bit_exact(ctx, m, k, rank):
     a = (rng.standard_normal((rank, k)) * 0.05).astype(np.float32)
     got = host(ctx.lora_mid(dev(x), dev(a)))
     assert bits_equal(got, dq8o.lora_mid(x, a, threads=4))
+
+
+def same_nan(got, want):
+    """Bit-equal outside NaNs, NaN at the same positions (payloads differ between x86 and the GPU)."""
+    got, want = np.asarray(got), np.asarray(want)
+    nan = np.isnan(want)
+    return got.shape == want.shape and np.array_equal(np.isnan(got), nan) and \
+        got[~nan].tobytes() == want[~nan].tobytes()
+
+
+@pytest.mark.parametrize("m,k,rank", [(24, 2048, 16), (37, 520, 20), (9, 131, 5)])
+def test_lora_mid_special_values(ctx, m, k, rank):
+    # denormal inputs, products that underflow into (or below) the denormal
+    # range, zeros of both signs (rows of -0.0 products sum to +0.0 lane sums),
+    # overflow to infinity and NaN inputs, each in its own rows
+    rng = np.random.default_rng(k + rank)
+    x = make_x(rng, m, k)
+    a = (rng.standard_normal((rank, k)) * 0.05).astype(np.float32)
+    tiny = np.array([1, 7, 0x7FFFFF, 0x400000], np.uint32).view(np.float32)
+    x[0] = rng.choice(tiny, size=k) * rng.choice([-1, 1], size=k).astype(np.float32)
+    x[1] = (rng.standard_normal(k) * 1e-20).astype(np.float32)
+    a[0] = (rng.standard_normal(k) * 1e-20).astype(np.float32)
+    x[2] = -0.0
+    x[3, ::3] = -0.0
+    x[4] = 0.0
+    x[5, k // 2] = 3e38
+    a[1 % rank, k // 2] = 1e5
+    x[6, k // 3] = np.inf
+    x[7, 1] = np.nan
+    a[rank - 1, k - 1] = -np.inf
+    x[8] = np.float32(1e19) * rng.choice([-1, 1], size=k).astype(np.float32)
+    got = host(ctx.lora_mid(dev(x), dev(a)))
+    want = dq8o.lora_mid(x, a, threads=4)
+    assert same_nan(got, want)
+    assert np.isinf(want).any() and np.isnan(want).any()
+
+
+@pytest.mark.parametrize("m,k,rank", [(24, 2048, 16), (130, 1000, 40), (8, 4, 3)])
+def test_lora_mid_unaligned_buffers(ctx, m, k, rank):
+    # x and A that are not 16-byte aligned take the plain-memory kernel; both
+    # kernels give the oracle's bits
+    rng = np.random.default_rng(m + k)
+    x = make_x(rng, m, k)
+    a = (rng.standard_normal((rank, k)) * 0.05).astype(np.float32)
+    want = dq8o.lora_mid(x, a, threads=4)
+    xf = torch.zeros(m * k + 1, dtype=torch.float32, device="cuda")
+    af = torch.zeros(rank * k + 3, dtype=torch.float32, device="cuda")
+    xs, as_ = xf[1:].view(m, k), af[3:].view(rank, k)
+    xs.copy_(dev(x))
+    as_.copy_(dev(a))
+    assert xs.data_ptr() % 16 != 0 and as_.data_ptr() % 16 != 0
+    assert bits_equal(host(ctx.lora_mid(xs, as_)), want)
+    assert bits_equal(host(ctx.lora_mid(dev(x), dev(a))), want)
 
 
 # (m, k, n, rank): skinny (m <= 32, short and long K) and wide kernels; ranks
