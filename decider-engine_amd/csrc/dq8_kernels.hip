@@ -47,6 +47,12 @@ __device__ __forceinline__ v32f mfma_k1(float a, float b, v32f c) {
 __device__ __forceinline__ v16f mfma_k2(float a, float b, v16f c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
+// 16 outer products of 4 x 4 (v_mfma_f32_4x4x1_16b_f32): block b takes A and
+// B from lanes 4b..4b+3, output element v of lane 4b + j is A[v] * B[j]; with
+// C = 0 every element is one product rounded once.
+__device__ __forceinline__ v4f mfma_k1_4(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ v32f concat(v16i lo, v16i hi) {
   v16f a = __builtin_bit_cast(v16f, lo), b = __builtin_bit_cast(v16f, hi);
   return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20,
@@ -723,20 +729,66 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       auto sw = [](int r, int i) { return r * 16 + (i ^ ((r >> 2) & 15)); };
       if (staged) {
         lds_barrier();  // every wave is done reading the ring
-        // all loads first (one memory latency), then the LDS writes
-        static_assert(WROWS <= 64 && WCOLS <= 64, "one row and one column per lane");
-        const float* gm = P.lmid + (size_t)min(mw + (lane % WROWS), P.m - 1) * P.rank;
-        const float* gb = P.lb + (size_t)min(nw + (lane % WCOLS), P.n - 1) * P.rank;
-        float vm[16], vb[16];
+        // The wave's mid rows mw.. and b rows nw.. are contiguous runs of
+        // WROWS * rank and WCOLS * rank floats: the lanes load them together
+        // (each load instruction covers whole cache lines), all loads first,
+        // then the LDS writes.  Rows past m or n read the last row instead.
+        static_assert(WROWS <= 64 && WCOLS <= 64, "at most 64 rows and columns per wave");
+        const int rk = P.rank;
+        if (rk == 16 && ((size_t)P.lmid & 15) == 0 && ((size_t)P.lb & 15) == 0) {
+          constexpr int TM = WROWS / 16, TB = WCOLS / 16;  // float4 per lane
+          v4f vm[TM], vb[TB];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          vm[i] = i < P.rank ? gm[i] : 0.0f;
-          vb[i] = i < P.rank ? gb[i] : 0.0f;
-        }
+          for (int t = 0; t < TM; ++t) {
+            const int e = 64 * t + lane;  // float4 index: row e/4, inputs 4(e%4)..+3
+            vm[t] = *reinterpret_cast<const v4f*>(P.lmid + (size_t)min(mw + (e >> 2), P.m - 1) * 16 + 4 * (e & 3));
+          }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          if (lane < WROWS) lmid[sw(lane, i)] = vm[i];
-          if (lane < WCOLS) lbw[sw(lane, i)] = vb[i];
+          for (int t = 0; t < TB; ++t) {
+            const int e = 64 * t + lane;
+            vb[t] = *reinterpret_cast<const v4f*>(P.lb + (size_t)min(nw + (e >> 2), P.n - 1) * 16 + 4 * (e & 3));
+          }
+#pragma unroll
+          for (int t = 0; t < TM; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int e = 64 * t + lane;
+              lmid[sw(e >> 2, 4 * (e & 3) + q)] = vm[t][q];
+            }
+#pragma unroll
+          for (int t = 0; t < TB; ++t)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int e = 64 * t + lane;
+              lbw[sw(e >> 2, 4 * (e & 3) + q)] = vb[t][q];
+            }
+        } else {
+          // element e of a run is row e / rank, input e % rank; with e < 1024
+          // and rank <= 16, (e + 0.5) / rank lies at least 1/32 from an integer,
+          // so the float quotient truncates to the exact row
+          const float inv = 1.0f / (float)rk;
+          auto row_of = [&](int e) { return (int)(((float)e + 0.5f) * inv); };
+          float vm[WROWS / 4], vb[WCOLS / 4];  // up to 16 * rows / 64 floats per lane
+#pragma unroll
+          for (int t = 0; t < WROWS / 4; ++t) {
+            const int e = 64 * t + lane, row = row_of(e);
+            vm[t] = row < WROWS ? P.lmid[(size_t)min(mw + row, P.m - 1) * rk + (e - row * rk)] : 0.0f;
+          }
+#pragma unroll
+          for (int t = 0; t < WCOLS / 4; ++t) {
+            const int e = 64 * t + lane, row = row_of(e);
+            vb[t] = row < WCOLS ? P.lb[(size_t)min(nw + row, P.n - 1) * rk + (e - row * rk)] : 0.0f;
+          }
+#pragma unroll
+          for (int t = 0; t < WROWS / 4; ++t) {
+            const int e = 64 * t + lane, row = row_of(e);
+            if (row < WROWS) lmid[sw(row, e - row * rk)] = vm[t];
+          }
+#pragma unroll
+          for (int t = 0; t < WCOLS / 4; ++t) {
+            const int e = 64 * t + lane, row = row_of(e);
+            if (row < WCOLS) lbw[sw(row, e - row * rk)] = vb[t];
+          }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's copies are visible to it
       }
@@ -750,9 +802,43 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 #pragma unroll
           for (int v = 0; v < 16; ++v) base[v] = s[j][16 * bk + v];
           if (staged) {
-            base = lora_term(base, zero16, P.rank, P.lscale, [&](int i) {
-              return mfma_k2(k0 ? lmid[sw(r, i)] : 0.0f, k0 ? lbw[sw(c, i)] : 0.0f, zero16);
-            });
+            // The block splits into 4 slices of 4 rows (8u + 4(l/32) + 0..3 for
+            // lane l, elements 4u..4u+3 of the block): one
+            // v_mfma_f32_4x4x1_16b_f32 forms a slice's products for one index,
+            // A lane l = mid[row 8u + 4(l/32) + l%4], B lane l = b[col l%32],
+            // so every slice sums on its own in 4 registers.
+            const float* rm[4];
+            int xm[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int ar = (RT == 2 ? 32 * bk : 0) + 8 * u + 4 * (lane >> 5) + (lane & 3);
+              rm[u] = lmid + 16 * ar;
+              xm[u] = (ar >> 2) & 15;
+            }
+            const float* rb = lbw + 16 * c;
+            const int xb = (c >> 2) & 15;
+            const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+            v16f sum;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              auto prod = [&](int i) { return mfma_k1_4(rm[u][i ^ xm[u]], rb[i ^ xb], zero4); };
+              v4f su;
+              if (P.rank == 16) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                  const v4f ln = prod(i) + prod(8 + i);
+                  su = i == 0 ? ln : su + ln;
+                }
+              } else {
+                // rank < 16: the lane sums are the products themselves, then
+                // the tail, all in index order from the first product
+                su = zero4;
+                for (int i = 0; i < P.rank; ++i) su = i == 0 ? prod(0) : su + prod(i);
+              }
+#pragma unroll
+              for (int v = 0; v < 4; ++v) sum[4 * u + v] = su[v];
+            }
+            base = base + P.lscale * (sum + zero16);
           } else {
             const float* lm = P.lmid + (size_t)min(mw + r, P.m - 1) * P.rank;
             const float* lbc = P.lb + (size_t)min(nw + c, P.n - 1) * P.rank;
@@ -811,9 +897,6 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 // no output of such a row or group is stored.
 __device__ __forceinline__ v4i mfma_i8_16(v4i a, v4i b, v4i c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ v4f mfma_k1_4(float a, float b, v4f c) {
-  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, c, 0, 0, 0);
 }
 
 // LDS bytes of the skinny kernel: the short-K preload (16 steps of activation

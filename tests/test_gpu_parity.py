@@ -533,6 +533,31 @@ def test_linear_lora_bit_exact(ctx, m, k, n, rank):
     assert bits_equal(cols, np.ascontiguousarray(want.T))
 
 
+@pytest.mark.parametrize("rank", [16, 15, 5, 1])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_linear_lora_wide_operand_staging(ctx, rank, aligned):
+    # The wide kernel copies a wave's mid and lora_B rows into LDS before the
+    # adapter products: 16-byte loads when rank == 16 and both buffers are
+    # 16-byte aligned, element loads otherwise; ragged m and n clamp the rows.
+    rng = np.random.default_rng(rank * 2 + aligned)
+    m, k, n = 130, 256, 200
+    x, wv, ws, a, b, bias = _lora_case(rng, m, k, n, rank)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    mid0 = ctx.lora_mid(dev(x), dev(a))
+    if aligned:
+        mid, bt = mid0, dev(b)
+    else:
+        mf = torch.zeros(m * rank + 1, dtype=torch.float32, device="cuda")
+        bf = torch.zeros(n * rank + 3, dtype=torch.float32, device="cuda")
+        mid, bt = mf[1:].view(m, rank), bf[3:].view(n, rank)
+        mid.copy_(mid0)
+        bt.copy_(dev(b))
+        assert mid.data_ptr() % 16 != 0 and bt.data_ptr() % 16 != 0
+    got = host(ctx.linear_lora(h, q, s, dq8.Lora(mid, bt, 0.625), bias=dev(bias)))
+    assert bits_equal(got, dq8o.linear_lora(x, wv, ws, a, b, 0.625, bias=bias, threads=4))
+
+
 def test_linear_lora_swiglu_epilogue(ctx):
     rng = np.random.default_rng(11)
     m, k, n, rank = 24, 2048, 96, 16
