@@ -4,9 +4,81 @@
 #include "dq8_st.h"
 
 #include <algorithm>
+#include <atomic>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
 #include <new>
 #include <stdint.h>
 #include <string.h>
+#include <thread>
+#include <vector>
+
+namespace {
+
+// Host threads that fill a pinned staging buffer in parallel pieces: a read of
+// a page-cached file is bound by one core's copy rate, well below the
+// host-to-device copy.  run_parts(parts, job) runs job(1..parts-1) on the
+// workers and job(0) on the caller, and returns when all have finished.
+class FillPool {
+ public:
+  explicit FillPool(int workers) {
+    try {
+      for (int i = 0; i < workers; ++i) threads_.emplace_back([this] { serve(); });
+    } catch (...) {
+      shut_down();  // the threads already started must not outlive the object
+      throw;
+    }
+  }
+  ~FillPool() { shut_down(); }
+  int workers() const { return (int)threads_.size(); }
+  void shut_down() {
+    {
+      std::lock_guard<std::mutex> lock(m_);
+      stop_ = true;
+    }
+    wake_.notify_all();
+    for (std::thread& t : threads_) t.join();
+    threads_.clear();
+  }
+  void run_parts(int parts, const std::function<void(int)>& job) {
+    {
+      std::lock_guard<std::mutex> lock(m_);
+      job_ = &job;
+      parts_ = parts;
+      next_ = 1;
+      pending_ = parts - 1;
+    }
+    wake_.notify_all();
+    job(0);
+    std::unique_lock<std::mutex> lock(m_);
+    done_.wait(lock, [this] { return pending_ == 0; });
+    job_ = nullptr;
+  }
+
+ private:
+  void serve() {
+    std::unique_lock<std::mutex> lock(m_);
+    for (;;) {
+      wake_.wait(lock, [this] { return stop_ || next_ < parts_; });
+      if (stop_) return;
+      const int p = next_++;
+      const std::function<void(int)>* job = job_;
+      lock.unlock();
+      (*job)(p);
+      lock.lock();
+      if (--pending_ == 0) done_.notify_one();
+    }
+  }
+  std::mutex m_;
+  std::condition_variable wake_, done_;
+  std::vector<std::thread> threads_;
+  const std::function<void(int)>* job_ = nullptr;
+  int parts_ = 0, next_ = 0, pending_ = 0;
+  bool stop_ = false;
+};
+
+}  // namespace
 
 struct dq8_ctx {
   int device;
@@ -23,6 +95,13 @@ struct dq8_ctx {
   // and the events of the copies out of them (created on first use).
   void* staging[2] = {nullptr, nullptr};
   hipEvent_t staged[2] = {nullptr, nullptr};
+  FillPool* fillers = nullptr;  // threads that fill the staging buffers (created on first use)
+  // Device buffers of weight loads: the stored elements, and the quantized
+  // values and scales before the repack.  Grow, never shrink.
+  void* load_raw = nullptr;
+  size_t load_raw_bytes = 0;
+  void* load_tmp = nullptr;
+  size_t load_tmp_bytes = 0;
 };
 
 struct dq8_weights {
@@ -398,13 +477,18 @@ dq8::FProj make_fproj(const dq8::Weights& w, const float* x, size_t m, const flo
 // ------------------------------------------------------------- weight loads
 
 constexpr size_t kStagingBytes = 8u << 20;
+#ifndef DQ8_FILL_THREADS
+#define DQ8_FILL_THREADS 4
+#endif
+constexpr int kFillThreads = DQ8_FILL_THREADS;  // the caller and kFillThreads - 1 pool threads
+constexpr size_t kFillPiece = 1u << 20;
 
 // Copies `bytes` bytes of a host source to device memory dst through the
 // context's two pinned staging buffers: fill(buffer, offset, count) writes
 // source bytes [offset, offset + count) into a buffer (a memcpy or a file
 // read) while the other buffer's copy is in flight.  On failure, copies
-// already queued may still be running: the caller synchronizes `s` before it
-// frees dst.
+// already queued may still be running: the caller synchronizes `s` before dst
+// is reused.
 template <typename Fill>
 dq8_status stage_to_device(dq8_ctx* ctx, uint8_t* dst, size_t bytes, hipStream_t s, Fill fill) {
   for (int b = 0; b < 2; ++b) {
@@ -416,12 +500,31 @@ dq8_status stage_to_device(dq8_ctx* ctx, uint8_t* dst, size_t bytes, hipStream_t
       return DQ8_ERR_DEVICE;
     }
   }
+  if (!ctx->fillers && bytes > kFillPiece && kFillThreads > 1) {
+    try {
+      ctx->fillers = new FillPool(kFillThreads - 1);
+    } catch (...) {
+      ctx->fillers = nullptr;  // no threads: the caller fills alone
+    }
+  }
+  // one staging chunk, filled in pieces of at least kFillPiece bytes on the pool
+  auto fill_chunk = [&](uint8_t* buf, size_t off, size_t count) -> bool {
+    const int parts = ctx->fillers ? (int)std::min<size_t>(kFillThreads, count / kFillPiece) : 1;
+    if (parts <= 1) return fill(buf, off, count);
+    const size_t piece = (count / parts + 4095) & ~(size_t)4095;
+    std::atomic<bool> ok{true};
+    ctx->fillers->run_parts(parts, [&](int p) {
+      const size_t o = (size_t)p * piece;
+      if (o < count && !fill(buf + o, off + o, std::min(piece, count - o))) ok = false;
+    });
+    return ok;
+  };
   size_t i = 0;
   for (size_t off = 0; off < bytes; off += kStagingBytes, ++i) {
     const int b = (int)(i & 1);
     const size_t count = std::min(kStagingBytes, bytes - off);
     if (i >= 2 && hipEventSynchronize(ctx->staged[b]) != hipSuccess) return DQ8_ERR_DEVICE;
-    if (!fill(ctx->staging[b], off, count)) return DQ8_ERR_IO;
+    if (!fill_chunk(static_cast<uint8_t*>(ctx->staging[b]), off, count)) return DQ8_ERR_IO;
     hipError_t e = hipMemcpyAsync(dst + off, ctx->staging[b], count, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipEventRecord(ctx->staged[b], s);
     if (e != hipSuccess) return from_hip(e);
@@ -438,22 +541,21 @@ bool raw_shape_ok(size_t n, size_t k) { return n && k && n <= (1u << 30) && k <=
 dq8_status quantize_raw_weights(dq8_ctx* ctx, const void* raw, int dtype, size_t n, size_t k, hipStream_t s,
                                 dq8_weights** out) {
   const size_t g = groups_of(k);
-  uint8_t* values = nullptr;
-  float* scales = nullptr;
+  const size_t vbytes = (n * k + 255) & ~(size_t)255;
+  dq8_status st = ensure_buffer(ctx->load_tmp, ctx->load_tmp_bytes, vbytes + n * g * sizeof(float));
+  if (st != DQ8_OK) return st;
+  uint8_t* values = static_cast<uint8_t*>(ctx->load_tmp);
+  float* scales = reinterpret_cast<float*>(values + vbytes);
   uint32_t flag = 0;
-  hipError_t e = hipMalloc(&values, n * k);
-  if (e == hipSuccess) e = hipMalloc(&scales, n * g * sizeof(float));
-  if (e == hipSuccess) e = dq8::launch_fill_u32(ctx->flag, 0, s);
+  hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
   if (e == hipSuccess)
     e = dq8::launch_quantize_raw(raw, dtype, (int)n, (int)k, (int8_t*)values, (int)k, scales, (int)g, ctx->flag, s);
   if (e == hipSuccess) e = hipMemcpyAsync(&flag, ctx->flag, sizeof(uint32_t), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
-  dq8_status st = from_hip(e);
+  st = from_hip(e);
   if (st == DQ8_OK && flag) st = DQ8_ERR_NONFINITE;
   if (st == DQ8_OK) st = dq8_weights_from_quantized(ctx, values, scales, n, k, s, out);
-  (void)hipStreamSynchronize(s);
-  (void)hipFree(values);
-  (void)hipFree(scales);
+  (void)hipStreamSynchronize(s);  // the repack has read the buffers before another load reuses them
   return st;
 }
 
@@ -462,13 +564,12 @@ dq8_status quantize_raw_weights(dq8_ctx* ctx, const void* raw, int dtype, size_t
 template <typename Fill>
 dq8_status load_weights(dq8_ctx* ctx, int dtype, size_t n, size_t k, hipStream_t s, dq8_weights** out, Fill fill) {
   const size_t bytes = n * k * raw_element_bytes(dtype);
-  uint8_t* raw = nullptr;
-  hipError_t e = hipMalloc(&raw, bytes);
-  if (e != hipSuccess) return from_hip(e);
-  dq8_status st = stage_to_device(ctx, raw, bytes, s, fill);
+  dq8_status st = ensure_buffer(ctx->load_raw, ctx->load_raw_bytes, bytes);
+  if (st != DQ8_OK) return st;
+  uint8_t* raw = static_cast<uint8_t*>(ctx->load_raw);
+  st = stage_to_device(ctx, raw, bytes, s, fill);
   if (st == DQ8_OK) st = quantize_raw_weights(ctx, raw, dtype, n, k, s, out);
   (void)hipStreamSynchronize(s);
-  (void)hipFree(raw);
   return st;
 }
 
@@ -522,6 +623,9 @@ dq8_status dq8_destroy(dq8_ctx* ctx) {
     if (ctx->staged[b]) (void)hipEventDestroy(ctx->staged[b]);
     if (ctx->staging[b]) (void)hipHostFree(ctx->staging[b]);
   }
+  delete ctx->fillers;
+  (void)hipFree(ctx->load_raw);
+  (void)hipFree(ctx->load_tmp);
   delete ctx;
   return DQ8_OK;
 }
