@@ -4,81 +4,9 @@
 #include "dq8_st.h"
 
 #include <algorithm>
-#include <atomic>
-#include <condition_variable>
-#include <functional>
-#include <mutex>
 #include <new>
 #include <stdint.h>
 #include <string.h>
-#include <thread>
-#include <vector>
-
-namespace {
-
-// Host threads that fill a pinned staging buffer in parallel pieces: a read of
-// a page-cached file is bound by one core's copy rate, well below the
-// host-to-device copy.  run_parts(parts, job) runs job(1..parts-1) on the
-// workers and job(0) on the caller, and returns when all have finished.
-class FillPool {
- public:
-  explicit FillPool(int workers) {
-    try {
-      for (int i = 0; i < workers; ++i) threads_.emplace_back([this] { serve(); });
-    } catch (...) {
-      shut_down();  // the threads already started must not outlive the object
-      throw;
-    }
-  }
-  ~FillPool() { shut_down(); }
-  int workers() const { return (int)threads_.size(); }
-  void shut_down() {
-    {
-      std::lock_guard<std::mutex> lock(m_);
-      stop_ = true;
-    }
-    wake_.notify_all();
-    for (std::thread& t : threads_) t.join();
-    threads_.clear();
-  }
-  void run_parts(int parts, const std::function<void(int)>& job) {
-    {
-      std::lock_guard<std::mutex> lock(m_);
-      job_ = &job;
-      parts_ = parts;
-      next_ = 1;
-      pending_ = parts - 1;
-    }
-    wake_.notify_all();
-    job(0);
-    std::unique_lock<std::mutex> lock(m_);
-    done_.wait(lock, [this] { return pending_ == 0; });
-    job_ = nullptr;
-  }
-
- private:
-  void serve() {
-    std::unique_lock<std::mutex> lock(m_);
-    for (;;) {
-      wake_.wait(lock, [this] { return stop_ || next_ < parts_; });
-      if (stop_) return;
-      const int p = next_++;
-      const std::function<void(int)>* job = job_;
-      lock.unlock();
-      (*job)(p);
-      lock.lock();
-      if (--pending_ == 0) done_.notify_one();
-    }
-  }
-  std::mutex m_;
-  std::condition_variable wake_, done_;
-  std::vector<std::thread> threads_;
-  const std::function<void(int)>* job_ = nullptr;
-  int parts_ = 0, next_ = 0, pending_ = 0;
-  bool stop_ = false;
-};
-
-}  // namespace
 
 struct dq8_ctx {
   int device;
@@ -95,7 +23,6 @@ struct dq8_ctx {
   // and the events of the copies out of them (created on first use).
   void* staging[2] = {nullptr, nullptr};
   hipEvent_t staged[2] = {nullptr, nullptr};
-  FillPool* fillers = nullptr;  // threads that fill the staging buffers (created on first use)
   // Device buffers of weight loads: the stored elements, and the quantized
   // values and scales before the repack.  Grow, never shrink.
   void* load_raw = nullptr;
@@ -477,11 +404,6 @@ dq8::FProj make_fproj(const dq8::Weights& w, const float* x, size_t m, const flo
 // ------------------------------------------------------------- weight loads
 
 constexpr size_t kStagingBytes = 8u << 20;
-#ifndef DQ8_FILL_THREADS
-#define DQ8_FILL_THREADS 4
-#endif
-constexpr int kFillThreads = DQ8_FILL_THREADS;  // the caller and kFillThreads - 1 pool threads
-constexpr size_t kFillPiece = 1u << 20;
 
 // Copies `bytes` bytes of a host source to device memory dst through the
 // context's two pinned staging buffers: fill(buffer, offset, count) writes
@@ -500,31 +422,12 @@ dq8_status stage_to_device(dq8_ctx* ctx, uint8_t* dst, size_t bytes, hipStream_t
       return DQ8_ERR_DEVICE;
     }
   }
-  if (!ctx->fillers && bytes > kFillPiece && kFillThreads > 1) {
-    try {
-      ctx->fillers = new FillPool(kFillThreads - 1);
-    } catch (...) {
-      ctx->fillers = nullptr;  // no threads: the caller fills alone
-    }
-  }
-  // one staging chunk, filled in pieces of at least kFillPiece bytes on the pool
-  auto fill_chunk = [&](uint8_t* buf, size_t off, size_t count) -> bool {
-    const int parts = ctx->fillers ? (int)std::min<size_t>(kFillThreads, count / kFillPiece) : 1;
-    if (parts <= 1) return fill(buf, off, count);
-    const size_t piece = (count / parts + 4095) & ~(size_t)4095;
-    std::atomic<bool> ok{true};
-    ctx->fillers->run_parts(parts, [&](int p) {
-      const size_t o = (size_t)p * piece;
-      if (o < count && !fill(buf + o, off + o, std::min(piece, count - o))) ok = false;
-    });
-    return ok;
-  };
   size_t i = 0;
   for (size_t off = 0; off < bytes; off += kStagingBytes, ++i) {
     const int b = (int)(i & 1);
     const size_t count = std::min(kStagingBytes, bytes - off);
     if (i >= 2 && hipEventSynchronize(ctx->staged[b]) != hipSuccess) return DQ8_ERR_DEVICE;
-    if (!fill_chunk(static_cast<uint8_t*>(ctx->staging[b]), off, count)) return DQ8_ERR_IO;
+    if (!fill(ctx->staging[b], off, count)) return DQ8_ERR_IO;
     hipError_t e = hipMemcpyAsync(dst + off, ctx->staging[b], count, hipMemcpyHostToDevice, s);
     if (e == hipSuccess) e = hipEventRecord(ctx->staged[b], s);
     if (e != hipSuccess) return from_hip(e);
@@ -623,7 +526,6 @@ dq8_status dq8_destroy(dq8_ctx* ctx) {
     if (ctx->staged[b]) (void)hipEventDestroy(ctx->staged[b]);
     if (ctx->staging[b]) (void)hipHostFree(ctx->staging[b]);
   }
-  delete ctx->fillers;
   (void)hipFree(ctx->load_raw);
   (void)hipFree(ctx->load_tmp);
   delete ctx;

@@ -17,10 +17,7 @@
  *     Weight handles are immutable after creation, so calls on different
  *     streams may share them.  One context must not be used by two host
  *     threads at once (its workspace is shared by its calls).
- *   - Threads: a context's first weight load from host memory or a file
- *     (dq8_weights_upload, dq8_st_load_weights) starts 3 host threads that fill
- *     its pinned staging buffers in parallel; dq8_destroy joins them.  No
- *     other call starts threads.
+ *   - The library starts no threads.
  *   - Weight loads keep their device buffers (stored elements, and values and
  *     scales before the repack) in the context, grown to the largest tensor
  *     loaded so far and freed by dq8_destroy.
