@@ -1009,26 +1009,55 @@ __device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, v4
     for (int rt = 0; rt < RT; ++rt) s[rt * CT + ct] = s[rt * CT + ct] + bias;
   }
   if (LORA && P.lora) {
+    const float* lm[RT];
+    const float* lbc[CT];
 #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const float* lm = P.lmid + (size_t)min(16 * rt + 4 * (lane >> 4) + (lane & 3), P.m - 1) * P.rank;
+    for (int rt = 0; rt < RT; ++rt)
+      lm[rt] = P.lmid + (size_t)min(16 * rt + 4 * (lane >> 4) + (lane & 3), P.m - 1) * P.rank;
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const float* lbc = P.lb + (size_t)min(c0 + 16 * ct + (lane & 15), P.n - 1) * P.rank;
-        if (P.rank <= 16) {
-          float am[16], bm[16];
+    for (int ct = 0; ct < CT; ++ct) lbc[ct] = P.lb + (size_t)min(c0 + 16 * ct + (lane & 15), P.n - 1) * P.rank;
+    if (P.rank <= 16) {
+      // every operand of the strip loaded up front (one memory latency), as
+      // 16-byte loads when rank is 16 and the rows are 16-byte aligned
+      float am[RT][16], bm[CT][16];
+      if (P.rank == 16 && ((size_t)P.lmid & 15) == 0 && ((size_t)P.lb & 15) == 0) {
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            am[i] = i < P.rank ? lm[i] : 0.0f;
-            bm[i] = i < P.rank ? lbc[i] : 0.0f;
+        for (int q = 0; q < 4; ++q) {
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            const v4f v = *reinterpret_cast<const v4f*>(lm[rt] + 4 * q);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) am[rt][4 * q + u] = v[u];
           }
-          s[rt * CT + ct] = lora_term16(s[rt * CT + ct], zero4, P.rank, P.lscale,
-                                        [&](int i) { return mfma_k1_4(am[i], bm[i], zero4); });
-        } else {
-          s[rt * CT + ct] = lora_term(s[rt * CT + ct], zero4, P.rank, P.lscale,
-                                      [&](int i) { return mfma_k1_4(lm[i], lbc[i], zero4); });
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) {
+            const v4f v = *reinterpret_cast<const v4f*>(lbc[ct] + 4 * q);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) bm[ct][4 * q + u] = v[u];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) am[rt][i] = i < P.rank ? lm[rt][i] : 0.0f;
+#pragma unroll
+          for (int ct = 0; ct < CT; ++ct) bm[ct][i] = i < P.rank ? lbc[ct][i] : 0.0f;
         }
       }
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+          s[rt * CT + ct] = lora_term16(s[rt * CT + ct], zero4, P.rank, P.lscale,
+                                        [&](int i) { return mfma_k1_4(am[rt][i], bm[ct][i], zero4); });
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct)
+          s[rt * CT + ct] = lora_term(s[rt * CT + ct], zero4, P.rank, P.lscale,
+                                      [&](int i) { return mfma_k1_4(lm[rt][i], lbc[ct][i], zero4); });
     }
   }
   int rows[E], cols[E];

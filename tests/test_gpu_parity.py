@@ -533,14 +533,16 @@ def test_linear_lora_bit_exact(ctx, m, k, n, rank):
     assert bits_equal(cols, np.ascontiguousarray(want.T))
 
 
+@pytest.mark.parametrize("m", [130, 24])
 @pytest.mark.parametrize("rank", [16, 15, 5, 1])
 @pytest.mark.parametrize("aligned", [True, False])
-def test_linear_lora_wide_operand_staging(ctx, rank, aligned):
-    # The wide kernel copies a wave's mid and lora_B rows into LDS before the
-    # adapter products: 16-byte loads when rank == 16 and both buffers are
-    # 16-byte aligned, element loads otherwise; ragged m and n clamp the rows.
-    rng = np.random.default_rng(rank * 2 + aligned)
-    m, k, n = 130, 256, 200
+def test_linear_lora_operand_staging(ctx, m, rank, aligned):
+    # Both kernels load the adapter operands (mid and lora_B rows) before the
+    # products: 16-byte loads when rank == 16 and both buffers are 16-byte
+    # aligned, element loads otherwise; ragged m and n clamp the rows.  130
+    # rows take the wide kernel (operands staged in LDS), 24 the skinny one.
+    rng = np.random.default_rng(rank * 2 + aligned + m)
+    k, n = 256, 200
     x, wv, ws, a, b, bias = _lora_case(rng, m, k, n, rank)
     h = ctx.weights_from_quantized(dev(wv), dev(ws))
     q, s = ctx.quantize(dev(x))
