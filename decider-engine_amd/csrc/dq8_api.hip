@@ -152,9 +152,18 @@ int xcd_rows_split(int row_tiles, int col_tiles, size_t a_bytes, size_t b_bytes)
 // Kernel kind of a projection (see launch_linear).
 int kind_of(const dq8::Weights&, size_t m) { return m > 32 ? 0 : m > 16 ? 2 : 1; }
 
+// A skinny launch whose projections would run on fewer one-wave strips than
+// this takes the 4-wave path for all of them: each wave then streams a quarter
+// of a strip's groups, so 4x the waves keep weight loads in flight.  Measured
+// at 24 rows: 2048x2048 9.8 -> 5.7 us, 2048x6144 9.9 -> 8.3 us; at 257 strips
+// (8224 outputs) and in a layer set's grouped launch (~930 strips) the
+// one-wave strips are faster (10.2 against 10.9 us; 30.5 against 40.1 us).
+constexpr long kSkinnyFewStrips = 256;
+long short_strips(const dq8::Weights& w) { return (w.n + dq8::skinny_cols(1) - 1) / dq8::skinny_cols(1); }
+
 // Place a filled projection in a launch of the given kernel kind: its first
 // wave/block, column strips, XCD split and the launch's running total.
-void place_proj(dq8::Proj& p, int kind, dq8::Batch& b) {
+void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips) {
   p.wave_begin = b.total_waves;
   p.xcd_gm = 0;
   p.nseg = 1;
@@ -164,8 +173,8 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b) {
     p.xcd_gm = xcd_rows_split(row_tiles, p.waves_n, (size_t)p.m * p.g, (size_t)p.n * p.g);
     b.total_waves += p.waves_n * row_tiles;
   } else {
-    p.waves_n = (p.n + dq8::skinny_cols(p.g) - 1) / dq8::skinny_cols(p.g);
-    p.nseg = dq8::skinny_segments(p.g);
+    p.nseg = dq8::skinny_segments(p.g, few_strips);
+    p.waves_n = (p.n + dq8::skinny_cols(p.nseg) - 1) / dq8::skinny_cols(p.nseg);
     const int per_block = 4 / p.nseg;
     b.total_waves += (p.waves_n + per_block - 1) / per_block;
   }
@@ -236,6 +245,15 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     b.count = b.total_waves = b.any_lora = 0;
     b.unless = unless;
   }
+  // one-wave strips each skinny launch would have (see kSkinnyFewStrips)
+  long strips[dq8::kKinds] = {};
+  for (size_t i = 0; i < count; ++i) {
+    const dq8_linear_item& it = items[i];
+    if (it.m == 0) continue;
+    const bool split = kind_of(it.w->w, it.m) == 0 && it.m <= 64 && it.layout == DQ8_ROWS;
+    const int kind = split ? 2 : kind_of(it.w->w, it.m);
+    strips[kind] += (split ? 2 : 1) * short_strips(it.w->w);
+  }
   size_t offset = 0;
   // Two passes: projections with long K (more than 32 groups) first, so their
   // blocks start when the launch does instead of trailing the short ones.
@@ -293,7 +311,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
         p.lmid += r0 * p.rank;
         b.any_lora = 1;
       }
-      place_proj(p, kind, b);
+      place_proj(p, kind, b, strips[kind] < kSkinnyFewStrips);
     }
   }
   for (int kind = 0; kind < dq8::kKinds; ++kind) {
@@ -372,7 +390,7 @@ dq8_status launch_one(const dq8::Weights& w, const WorkInputs& in, size_t m, con
   dq8::Proj& p = b.p[0];
   fill_proj(p, w, in.q, in.ldq, in.xs, in.ldxs, m, bias, out, nullptr, layout, epilogue, lora);
   const int kind = kind_of(w, m);
-  place_proj(p, kind, b);
+  place_proj(p, kind, b, short_strips(w) < kSkinnyFewStrips);
   return from_hip(dq8::launch_linear(b, kind, false, s));
 }
 

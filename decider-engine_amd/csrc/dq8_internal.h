@@ -45,7 +45,7 @@ struct Proj {
   int epilogue;       // 0 write, 1 add, 2 swiglu
   int layout;         // 0 rows [M][N], 1 columns [N][M]
   int wave_begin;     // first block of this projection in the launch
-  int waves_n;        // column strips (skinny: skinny_cols(g) wide, wide: one block tile wide)
+  int waves_n;        // column strips (skinny: skinny_cols(nseg) wide, wide: one block tile wide)
   int xcd_gm;         // wide: row bands of the per-XCD tile regions (1, 2, 4, 8), 0 = row-major order
   int nseg;           // skinny: waves per strip (1 or 4)
 };
@@ -102,8 +102,10 @@ constexpr int kKinds = 3;
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s);
 // Columns of a skinny strip for g groups (all rows), and the waves that share
 // a strip's groups (1 or 4).
-int skinny_cols(int g);
-int skinny_segments(int g);
+// Skinny kernel paths: 1 segment (one wave per strip, all groups; short K) or
+// 4 (a strip's groups split over 4 waves; long K, or launches with few strips).
+int skinny_segments(int g, bool few_strips);
+int skinny_cols(int nseg);  // strip width of a path
 // Block tile of the wide kernel (rows, columns); kColPad is a multiple of the columns.
 int wide_block_rows();
 int wide_block_cols();

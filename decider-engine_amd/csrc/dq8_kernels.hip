@@ -1791,8 +1791,11 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
 #endif
 // Short K (G <= 32) runs one wave per strip; longer K interleaves a strip's
 // groups over 4 waves.
-int skinny_segments(int g) { return g <= 32 ? 1 : 4; }
-int skinny_cols(int g) { return 16 * (skinny_segments(g) == 1 ? DQ8_SKINNY_CT : DQ8_SKINNY_CTL); }
+#ifndef DQ8_SKINNY_SHORT_MAX_G
+#define DQ8_SKINNY_SHORT_MAX_G 32
+#endif
+int skinny_segments(int g, bool few_strips) { return g <= DQ8_SKINNY_SHORT_MAX_G && !few_strips ? 1 : 4; }
+int skinny_cols(int nseg) { return 16 * (nseg == 1 ? DQ8_SKINNY_CT : DQ8_SKINNY_CTL); }
 int wide_block_rows() { return 32 * DQ8_WIDE_RT * DQ8_WIDE_WM; }
 int wide_block_cols() { return 32 * DQ8_WIDE_CT * DQ8_WIDE_WN; }
 

@@ -332,6 +332,62 @@ def test_linear_batch_question_layer_set(ctx):
         assert bits_equal(host(it.out), want)
 
 
+# A question's projections at full size: q, k, v, o, GDN in/out, FFN gate, up
+# (SwiGlu onto gate's output) and down (Add).  About 930 one-wave strips, so the
+# grouped launch keeps the short-K skinny path (small launches take the 4-wave
+# path); 9 rows take the 16-row kernel, 24 the 32-row one.
+FULL_LAYER = [("q", 2048, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 2048), ("gdn_in", 8224, 2048),
+              ("gdn_out", 2048, 2048), ("gate", 6144, 2048), ("up", 6144, 2048), ("down", 2048, 6144)]
+
+
+@pytest.mark.parametrize("m", [24, 9])
+def test_linear_batch_full_layer_set(ctx, m):
+    rng = np.random.default_rng(m + 1000)
+    weights = {}
+    for name, n, k in FULL_LAYER:
+        wv, ws = dq8o.quantize_weights(make_w(rng, n, k))
+        weights[name] = (wv, ws, ctx.weights_from_quantized(dev(wv), dev(ws)))
+    x = make_x(rng, m, 2048, kind="student")
+    xd = make_x(rng, m, 6144)
+    q, s = ctx.quantize(dev(x))
+    qd, sd = ctx.quantize(dev(xd))
+    resid = rng.standard_normal((m, 2048)).astype(np.float32)
+    outs = {name: dev(np.zeros((m, n), np.float32)) for name, n, _ in FULL_LAYER}
+    outs["down"] = dev(resid.copy())
+    items = [dq8.Item(weights[name][2], qd if name == "down" else q, sd if name == "down" else s, outs[name],
+                      epilogue=dq8.ADD if name == "down" else dq8.WRITE)
+             for name, _, _ in FULL_LAYER if name != "up"]
+    ctx.linear_batch(items)
+    # up after gate: its SwiGlu reads gate's stored output
+    ctx.linear_batch([dq8.Item(weights["up"][2], q, s, outs["gate"], epilogue=dq8.SWIGLU)])
+    for name, _, _ in FULL_LAYER:
+        wv, ws, _ = weights[name]
+        if name == "up":
+            continue
+        if name == "down":
+            want = dq8o.linear(xd, wv, ws, result=resid, epilogue=1, threads=8)
+        elif name == "gate":
+            gate = dq8o.linear(x, wv, ws, threads=8)
+            want = dq8o.linear(x, weights["up"][0], weights["up"][1], result=gate, epilogue=2, threads=8)
+        else:
+            want = dq8o.linear(x, wv, ws, threads=8)
+        assert bits_equal(host(outs[name]), want), name
+
+
+def test_skinny_short_path_single_projection_with_lora(ctx):
+    # 8224 outputs = 257 one-wave strips: a single projection on the short-K path,
+    # with a rank-16 adapter
+    rng = np.random.default_rng(8224)
+    m, k, n, rank = 24, 2048, 8224, 16
+    x, wv, ws, a, b, bias = _lora_case(rng, m, k, n, rank)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    lora = dq8.Lora(ctx.lora_mid(dev(x), dev(a)), dev(b), 0.25)
+    got = host(ctx.linear_lora(h, q, s, lora, bias=dev(bias)))
+    assert bits_equal(got, dq8o.linear_lora(x, wv, ws, a, b, 0.25, bias=bias, threads=8))
+    assert bits_equal(host(ctx.linear(h, q, s, bias=dev(bias))), dq8o.linear(x, wv, ws, bias=bias, threads=8))
+
+
 @pytest.mark.parametrize("tokens", [[24, 24], [24, 24, 24, 24], [24, 17, 31, 9, 24, 5, 30, 24], [24] * 16, [40]])
 def test_questions_stacked_rows_match_per_question_launches(ctx, tokens):
     # Continuation of several questions (lib.rs:512-528 runs them one after
