@@ -1470,6 +1470,9 @@ constexpr int kMidRows = 8, kMidJ = 16, kMidKT = 256, kMidStride = kMidKT + 8;
 #ifndef DQ8_MID_BATCH
 #define DQ8_MID_BATCH 8
 #endif
+#ifndef DQ8_MID_SMALL_M
+#define DQ8_MID_SMALL_M 32  // rows up to which k_lora_mid_small runs (0: never)
+#endif
 constexpr int kMidSlots = DQ8_MID_SLOTS, kMidLoads = 6;  // DMA loads per wave per tile
 constexpr int kMidBatch = DQ8_MID_BATCH;
 __global__ __launch_bounds__(256) void k_lora_mid_dma(const float* __restrict__ x, int m, int k,
@@ -1560,6 +1563,58 @@ __global__ __launch_bounds__(256) void k_lora_mid_dma(const float* __restrict__ 
       for (int e = full; e < k; ++e) sum = sum + xg[e] * ag[e];
       mid[(size_t)row * rank + j] = sum + 0.0f;
     }
+  }
+}
+
+// k_lora_mid_small<R, J>: few rows (m <= 32).  A block holds R whole rows of x
+// and J whole adapter rows in LDS, fetched by one round of direct global->LDS
+// loads (1 KB each; the block's 4 waves issue every 4th, at most 39 each), so
+// the memory latency is paid once; then the first R * J * 8 threads compute.  Lane l works on row r0 + (l/8)/J, adapter row j0 + (l/8)%J and lane
+// sum i = l%8: the chunks are summed in order on the VALU (one rounded product
+// and one rounded add each), then the 8 lane sums of a pair, in consecutive
+// lanes, are added in order from -0.0, then the tail elements.  Loads past a
+// row's end are clamped to its last 16 bytes and land in the row padding.
+// Requires k % 4 == 0, 16-byte aligned x and a, and roundup(k, 256) <= KR.
+template <int R, int J, int KR>
+__global__ __launch_bounds__(256) void k_lora_mid_small(const float* __restrict__ x, int m, int k,
+                                                             const float* __restrict__ a, int rank,
+                                                             float* __restrict__ mid) {
+  constexpr int NT = R * J * 8, NW = 4, RS = KR + 8;  // row stride: the 8 rows of a step in distinct banks
+  static_assert(NT % 64 == 0 && NT <= 256, "whole waves of one block");
+  static_assert((R + J) * ((KR + 255) / 256) <= 48 * NW, "at most 48 loads in flight per wave");
+  __shared__ __attribute__((aligned(16))) float lds[(R + J) * RS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int jblocks = (rank + J - 1) / J;
+  const int r0 = (int)(blockIdx.x / jblocks) * R, j0 = (int)(blockIdx.x % jblocks) * J;
+  const int segs = (k + 255) >> 8;  // 1 KB pieces per row
+  for (int t = w; t < (R + J) * segs; t += NW) {  // wave-uniform
+    const int row = t / segs, seg = t - row * segs;
+    const float* src = row < R ? x + (size_t)min(r0 + row, m - 1) * k : a + (size_t)min(j0 + row - R, rank - 1) * k;
+    const uint32_t off = 4u * (uint32_t)min(4 * lane, k - 4 - 256 * seg);  // k % 4 == 0: k - 256*seg >= 4
+    dma16s(src + 256 * seg, off, lds + row * RS + 256 * seg);
+  }
+  wait_vmcnt<0>();
+  lds_barrier();
+  if (tid >= NT) return;  // wave-uniform: NT is a multiple of 64
+  const int pr = tid >> 3, i = tid & 7, r = pr / J, j = pr - r * J;
+  const float* xs = lds + r * RS;
+  const float* as = lds + (R + j) * RS;
+  const int chunks = k >> 3;
+  float acc = 0.0f;
+  int c = 0;
+  for (; c + 8 <= chunks; c += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = acc + xs[8 * (c + u) + i] * as[8 * (c + u) + i];
+  }
+  for (; c < chunks; ++c) acc = acc + xs[8 * c + i] * as[8 * c + i];
+  float sum = -0.0f;
+#pragma unroll
+  for (int ii = 0; ii < 8; ++ii) sum = sum + __shfl(acc, (lane & ~7) + ii);
+  const int row = r0 + r, jr = j0 + j;
+  if (i == 0 && row < m && jr < rank) {
+    for (int e = 8 * chunks; e < k; ++e) sum = sum + xs[e] * as[e];
+    mid[(size_t)row * rank + jr] = sum + 0.0f;
   }
 }
 
@@ -1715,7 +1770,14 @@ hipError_t launch_linear_fp32(const FProj& p, hipStream_t s) {
 
 hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int rank, float* mid, hipStream_t s) {
   if (m == 0 || rank == 0) return hipSuccess;
-  if (k % 4 == 0 && ((size_t)x & 15) == 0 && ((size_t)a & 15) == 0) {
+  const bool dma = k % 4 == 0 && ((size_t)x & 15) == 0 && ((size_t)a & 15) == 0;
+  const int kr = (k + 255) & ~255;
+  if (dma && m <= DQ8_MID_SMALL_M && kr <= 6656) {
+    // 4 x rows and 2 adapter rows per block (6 rows in LDS: the fewest for a
+    // wave of lane sums); measured 6.1 us at 24 x 2048 rank 16 against 8.4 for
+    // 8 x 4 blocks and 8.2 for the tiled kernel, 14.3 against 20.8 at k = 6144
+    k_lora_mid_small<4, 2, 6656><<<(unsigned)((m + 3) / 4 * ((rank + 1) / 2)), 256, 0, s>>>(x, m, k, a, rank, mid);
+  } else if (dma) {
     const long blocks = (long)((m + kMidRows - 1) / kMidRows) * ((rank + kMidJ - 1) / kMidJ);
     k_lora_mid_dma<<<(unsigned)blocks, 256, 0, s>>>(x, m, k, a, rank, mid);
   } else {

@@ -481,13 +481,16 @@ def test_config1_single_linear_seed0_bit_exact(ctx):
 
 # ------------------------------------------------------------------- LoRA
 
-# The LDS-staged kernel takes k % 4 == 0 with 16-byte aligned rows; other
+# The LDS-staged kernels take k % 4 == 0 with 16-byte aligned rows; other
 # shapes take the plain-memory kernel.  Shapes cover ranks past one block of 16
 # adapter rows (full and partial), partial tiles of 256 inputs, k % 8 == 4
 # over several tiles, k with no full chunk of 8 (tail only) and full size.
 LORA_MID_SHAPES = [(1, 64, 1), (5, 131, 13), (24, 2048, 16), (67, 100, 3), (130, 2048, 16), (9, 7, 9), (4, 6144, 8),
                    (130, 2048, 40), (9, 256, 64), (300, 1000, 24), (16, 8, 17), (33, 4, 5), (8, 2052, 16),
-                   (2048, 2048, 16), (17, 264, 33)]
+                   (2048, 2048, 16), (17, 264, 33),
+                   # m <= 32: whole rows staged in LDS (4 x rows + 2 adapter rows per block) up to
+                   # k = 6656, beyond that the tiled kernel
+                   (32, 3328, 16), (32, 3332, 7), (20, 6656, 16), (5, 6660, 3), (31, 2048, 5), (32, 6144, 64)]
 
 
 @pytest.mark.parametrize("m,k,rank", LORA_MID_SHAPES)
