@@ -386,6 +386,68 @@ def run_lora_stack(args, torch, stream, build, run_step, step_ops, base_ms):
     }
 
 
+def run_skinny_lora(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, acts, launches):
+    """The questions of the skinny leg with a rank-r FP32 LoRA pair on every projection: per question the 9
+    middle products (dq8_lora_mid, few-rows kernel) and the grouped launch with adapters.  The plain and the
+    adapter questions are both captured in a HIP graph and replayed, so host submission of the extra calls is
+    not timed."""
+    M, rank = args.question_tokens, args.lora_rank
+    pairs = [((torch.randn((rank, k), generator=gen, device=dev) * 0.02).contiguous(),
+              (torch.randn((n, rank), generator=gen, device=dev) * 0.02).contiguous()) for _, n, k in shapes]
+    mids = [[torch.empty((M, rank), dtype=torch.float32, device=dev) for _ in shapes] for _ in acts]
+    keep, lora_launches = [], []
+    for qi in range(args.questions):
+        ws = copies[qi % len(copies)]
+        items = (dq8._Item * len(shapes))()
+        for j, (q, s, o, _) in enumerate(acts[qi]):
+            lr = dq8._Lora(mids[qi][j].data_ptr(), pairs[j][1].data_ptr(), rank, 0.5)
+            keep.append(lr)
+            items[j] = dq8._Item(ws[j].handle, q.data_ptr(), s.data_ptr(), M, None, o.data_ptr(), dq8.ROWS,
+                                 dq8.WRITE, ctypes.pointer(lr))
+        lora_launches.append(items)
+    sh = stream.cuda_stream
+
+    def call(st, what):
+        if st != 0:
+            raise dq8.Dq8Error(st, what)
+
+    def plain():
+        for items in launches:
+            call(lib.dq8_linear_batch(ctx.handle, items, len(shapes), sh), "dq8_linear_batch")
+
+    def adapters():
+        for qi, items in enumerate(lora_launches):
+            for j, (_, n, k) in enumerate(shapes):
+                call(lib.dq8_lora_mid(ctx.handle, acts[qi][j][3].data_ptr(), M, k, pairs[j][0].data_ptr(), rank,
+                                      mids[qi][j].data_ptr(), sh), "dq8_lora_mid")
+            call(lib.dq8_linear_batch(ctx.handle, items, len(shapes), sh), "dq8_linear_batch")
+
+    def graph_ms(fn):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for _ in range(args.skinny_reps):
+            g.replay()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / (args.skinny_reps * args.questions)
+
+    plain_ms, lora_ms = graph_ms(plain), graph_ms(adapters)
+    return {
+        "workload": f"the same questions with a rank-{rank} FP32 LoRA pair on every projection (9 middle products "
+                    f"+ the grouped launch with adapters per question; HIP graph replay)",
+        "ms_per_question": round(lora_ms, 5),
+        "plain_ms_per_question": round(plain_ms, 5),
+        "overhead_vs_plain": round(lora_ms / plain_ms - 1.0, 4),
+    }
+
+
 def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
     """16 questions x M tokens, one grouped launch per question over a layer's projections."""
     M = args.question_tokens
@@ -403,13 +465,13 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
         for _, n, k in shapes:
             x = torch.randn((M, k), generator=gen, device=dev)
             q, s = ctx.quantize(x)
-            per.append((q, s, torch.empty((M, n), dtype=torch.float32, device=dev)))
+            per.append((q, s, torch.empty((M, n), dtype=torch.float32, device=dev), x))
         acts.append(per)
     launches = []
     for qi in range(args.questions):
         ws = copies[qi % len(copies)]
         items = (dq8._Item * len(shapes))()
-        for j, (q, s, o) in enumerate(acts[qi]):
+        for j, (q, s, o, _) in enumerate(acts[qi]):
             items[j] = dq8._Item(ws[j].handle, q.data_ptr(), s.data_ptr(), M, None, o.data_ptr(), dq8.ROWS,
                                  dq8.WRITE)
         launches.append(items)
@@ -452,6 +514,7 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
     kernel_gbs = wbytes / (avg_launch * 1e-3) / 1e9
     stacked = run_stacked(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, wbytes,
                           total_ms / (reps * args.questions))
+    lora = run_skinny_lora(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, acts, launches)
     for ws in copies:
         for h in ws:
             h.free()
@@ -474,6 +537,7 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
             "bytes_per_launch": wbytes,
             "avg_launch_ms": round(avg_launch, 5),
         },
+        "lora": lora,
     }
 
 
