@@ -388,23 +388,26 @@ def run_lora_stack(args, torch, stream, build, run_step, step_ops, base_ms):
 
 def run_skinny_lora(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, acts, launches):
     """The questions of the skinny leg with a rank-r FP32 LoRA pair on every projection: per question the 9
-    middle products (dq8_lora_mid, few-rows kernel) and the grouped launch with adapters.  The plain and the
+    middle products (one dq8_lora_mid_batch launch, few-rows kernel) and the grouped launch with adapters.  The plain and the
     adapter questions are both captured in a HIP graph and replayed, so host submission of the extra calls is
     not timed."""
     M, rank = args.question_tokens, args.lora_rank
     pairs = [((torch.randn((rank, k), generator=gen, device=dev) * 0.02).contiguous(),
               (torch.randn((n, rank), generator=gen, device=dev) * 0.02).contiguous()) for _, n, k in shapes]
     mids = [[torch.empty((M, rank), dtype=torch.float32, device=dev) for _ in shapes] for _ in acts]
-    keep, lora_launches = [], []
+    keep, lora_launches, mid_items = [], [], []
     for qi in range(args.questions):
         ws = copies[qi % len(copies)]
         items = (dq8._Item * len(shapes))()
-        for j, (q, s, o, _) in enumerate(acts[qi]):
+        mi = (dq8._MidItem * len(shapes))()
+        for j, (q, s, o, x) in enumerate(acts[qi]):
             lr = dq8._Lora(mids[qi][j].data_ptr(), pairs[j][1].data_ptr(), rank, 0.5)
             keep.append(lr)
             items[j] = dq8._Item(ws[j].handle, q.data_ptr(), s.data_ptr(), M, None, o.data_ptr(), dq8.ROWS,
                                  dq8.WRITE, ctypes.pointer(lr))
+            mi[j] = dq8._MidItem(x.data_ptr(), M, shapes[j][2], pairs[j][0].data_ptr(), rank, mids[qi][j].data_ptr())
         lora_launches.append(items)
+        mid_items.append(mi)
     sh = stream.cuda_stream
 
     def call(st, what):
@@ -417,9 +420,8 @@ def run_skinny_lora(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies
 
     def adapters():
         for qi, items in enumerate(lora_launches):
-            for j, (_, n, k) in enumerate(shapes):
-                call(lib.dq8_lora_mid(ctx.handle, acts[qi][j][3].data_ptr(), M, k, pairs[j][0].data_ptr(), rank,
-                                      mids[qi][j].data_ptr(), sh), "dq8_lora_mid")
+            # the question's 9 middle products in one grouped launch, then the projections
+            call(lib.dq8_lora_mid_batch(ctx.handle, mid_items[qi], len(shapes), sh), "dq8_lora_mid_batch")
             call(lib.dq8_linear_batch(ctx.handle, items, len(shapes), sh), "dq8_linear_batch")
 
     def graph_ms(fn):
@@ -440,8 +442,8 @@ def run_skinny_lora(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies
 
     plain_ms, lora_ms = graph_ms(plain), graph_ms(adapters)
     return {
-        "workload": f"the same questions with a rank-{rank} FP32 LoRA pair on every projection (9 middle products "
-                    f"+ the grouped launch with adapters per question; HIP graph replay)",
+        "workload": f"the same questions with a rank-{rank} FP32 LoRA pair on every projection (one grouped launch "
+                    f"of the 9 middle products + the grouped launch with adapters per question; HIP graph replay)",
         "ms_per_question": round(lora_ms, 5),
         "plain_ms_per_question": round(plain_ms, 5),
         "overhead_vs_plain": round(lora_ms / plain_ms - 1.0, 4),

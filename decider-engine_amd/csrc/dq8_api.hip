@@ -698,16 +698,62 @@ dq8_status dq8_linear_lora(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, 
   return run_linear(ctx, &it, 1, nullptr, (hipStream_t)stream);
 }
 
-dq8_status dq8_lora_mid(dq8_ctx* ctx, const float* x, size_t m, size_t k, const float* a, size_t rank, float* mid,
-                        void* stream) {
-  if (!ctx) return DQ8_ERR_ARG;
+}  // extern "C"
+
+namespace {
+// Arguments of one middle product (m == 0 or rank == 0: nothing to do).
+dq8_status check_mid(const float* x, size_t m, size_t k, const float* a, size_t rank, const float* mid) {
   if (m == 0 || rank == 0) return DQ8_OK;
   if (!x || !a || !mid) return DQ8_ERR_ARG;
   if (k == 0 || m > (1u << 30) || k > (1u << 30) || rank > (1u << 20) || m * k > ((size_t)1 << 40) ||
       rank * k > ((size_t)1 << 40) || ((m + 7) / 8) * ((rank + 15) / 16) >= ((size_t)1 << 23))
     return DQ8_ERR_SHAPE;  // the last bound keeps the grid under 2^32 work-items
+  return DQ8_OK;
+}
+}  // namespace
+
+extern "C" {
+
+dq8_status dq8_lora_mid(dq8_ctx* ctx, const float* x, size_t m, size_t k, const float* a, size_t rank, float* mid,
+                        void* stream) {
+  if (!ctx) return DQ8_ERR_ARG;
+  dq8_status st = check_mid(x, m, k, a, rank, mid);
+  if (st != DQ8_OK || m == 0 || rank == 0) return st;
   DeviceGuard guard(ctx->device);
   return from_hip(dq8::launch_lora_mid(x, (int)m, (int)k, a, (int)rank, mid, (hipStream_t)stream));
+}
+
+dq8_status dq8_lora_mid_batch(dq8_ctx* ctx, const dq8_lora_mid_item* items, size_t count, void* stream) {
+  if (!ctx || (count && !items)) return DQ8_ERR_ARG;
+  for (size_t i = 0; i < count; ++i) {  // every item is checked before anything runs
+    dq8_status st = check_mid(items[i].x, items[i].m, items[i].k, items[i].a, items[i].rank, items[i].mid);
+    if (st != DQ8_OK) return st;
+  }
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = (hipStream_t)stream;
+  dq8::MidBatch b;
+  b.count = 0;
+  long blocks = 0;
+  for (size_t i = 0; i < count; ++i) {
+    const dq8_lora_mid_item& it = items[i];
+    if (it.m == 0 || it.rank == 0) continue;
+    const int m = (int)it.m, k = (int)it.k, rank = (int)it.rank;
+    if (!dq8::lora_mid_small_ok(it.x, m, k, it.a)) {  // other kernels: a launch of its own
+      hipError_t e = dq8::launch_lora_mid(it.x, m, k, it.a, rank, it.mid, s);
+      if (e != hipSuccess) return from_hip(e);
+      continue;
+    }
+    const long nb = dq8::lora_mid_small_blocks(m, rank);
+    if (b.count == dq8::kMaxMids || blocks + nb >= ((long)1 << 23)) {
+      hipError_t e = dq8::launch_lora_mid_batch(b, blocks, s);
+      if (e != hipSuccess) return from_hip(e);
+      b.count = 0;
+      blocks = 0;
+    }
+    b.it[b.count++] = {it.x, it.a, it.mid, m, k, rank, (int)blocks};
+    blocks += nb;
+  }
+  return from_hip(dq8::launch_lora_mid_batch(b, blocks, s));
 }
 
 dq8_status dq8_linear_batch(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, void* stream) {

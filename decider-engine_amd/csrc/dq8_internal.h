@@ -10,6 +10,7 @@ namespace dq8 {
 constexpr int kGroup = 64;        // reference group width (weights.rs:119, tensor.rs:329)
 constexpr int kFragBytes = 1024;  // one MFMA operand fragment: 64 lanes x 16 bytes
 constexpr int kMaxBatch = 16;     // projections per launch
+constexpr int kMaxMids = 32;      // LoRA middle products per grouped launch
 constexpr int kColPad = 256;      // weights are padded to a multiple of this many outputs
 // Stored element types of raw weights (values of dq8_dtype).
 constexpr int kDtypeF32 = 0, kDtypeBF16 = 1, kDtypeF16 = 2;
@@ -60,6 +61,20 @@ struct Batch {
   const uint32_t* unless;
 };
 
+// LoRA middle products of several (x, A) pairs in one launch of the few-rows
+// kernel (lora_mid_small_ok items only).
+struct MidItem {
+  const float* x;
+  const float* a;
+  float* mid;
+  int m, k, rank;
+  int block_begin;  // first block of the item in the launch
+};
+struct MidBatch {
+  MidItem it[kMaxMids];
+  int count;
+};
+
 // One projection of the FP32 path (Projection::columns_tiled, tensor.rs:206-269)
 // over fp32 inputs x [m][k] and dequantized int8 weights.
 struct FProj {
@@ -96,6 +111,9 @@ hipError_t launch_or_u32(uint32_t* dst, const uint32_t* src, hipStream_t s);
 hipError_t launch_linear_fp32(const FProj& p, hipStream_t s);
 // LoRA middle product mid [m][rank] = dot_scores(x_r, a_j) + 0.0 (x [m][k], a [rank][k]).
 hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int rank, float* mid, hipStream_t s);
+bool lora_mid_small_ok(const float* x, int m, int k, const float* a);  // the few-rows kernel takes it
+long lora_mid_small_blocks(int m, int rank);
+hipError_t launch_lora_mid_batch(const MidBatch& b, long blocks, hipStream_t s);
 // Kind: 0 wide (M > 32), 1 skinny (M <= 16), 2 skinny (16 < M <= 32).  dots
 // selects the debug kernel.
 constexpr int kKinds = 3;

@@ -1575,18 +1575,18 @@ __global__ __launch_bounds__(256) void k_lora_mid_dma(const float* __restrict__ 
 // lanes, are added in order from -0.0, then the tail elements.  Loads past a
 // row's end are clamped to its last 16 bytes and land in the row padding.
 // Requires k % 4 == 0, 16-byte aligned x and a, and roundup(k, 256) <= KR.
+constexpr int kSmallR = 4, kSmallJ = 2, kSmallKR = 6656;  // the one configuration in use
+constexpr int kSmallRS = kSmallKR + 8;                     // row stride: the 8 rows of a step in distinct banks
 template <int R, int J, int KR>
-__global__ __launch_bounds__(256) void k_lora_mid_small(const float* __restrict__ x, int m, int k,
-                                                             const float* __restrict__ a, int rank,
-                                                             float* __restrict__ mid) {
-  constexpr int NT = R * J * 8, NW = 4, RS = KR + 8;  // row stride: the 8 rows of a step in distinct banks
+__device__ __forceinline__ void lora_mid_small(const float* __restrict__ x, int m, int k, const float* __restrict__ a,
+                                               int rank, float* __restrict__ mid, int block, float* lds) {
+  constexpr int NT = R * J * 8, NW = 4, RS = KR + 8;
   static_assert(NT % 64 == 0 && NT <= 256, "whole waves of one block");
   static_assert((R + J) * ((KR + 255) / 256) <= 48 * NW, "at most 48 loads in flight per wave");
-  __shared__ __attribute__((aligned(16))) float lds[(R + J) * RS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int jblocks = (rank + J - 1) / J;
-  const int r0 = (int)(blockIdx.x / jblocks) * R, j0 = (int)(blockIdx.x % jblocks) * J;
+  const int r0 = (block / jblocks) * R, j0 = (block % jblocks) * J;
   const int segs = (k + 255) >> 8;  // 1 KB pieces per row
   for (int t = w; t < (R + J) * segs; t += NW) {  // wave-uniform
     const int row = t / segs, seg = t - row * segs;
@@ -1616,6 +1616,22 @@ __global__ __launch_bounds__(256) void k_lora_mid_small(const float* __restrict_
     for (int e = 8 * chunks; e < k; ++e) sum = sum + xs[e] * as[e];
     mid[(size_t)row * rank + jr] = sum + 0.0f;
   }
+}
+__global__ __launch_bounds__(256) void k_lora_mid_small(const float* __restrict__ x, int m, int k,
+                                                        const float* __restrict__ a, int rank, float* __restrict__ mid) {
+  __shared__ __attribute__((aligned(16))) float lds[(kSmallR + kSmallJ) * kSmallRS];
+  lora_mid_small<kSmallR, kSmallJ, kSmallKR>(x, m, k, a, rank, mid, (int)blockIdx.x, lds);
+}
+// Several middle products in one launch: block b belongs to the last item whose
+// first block is <= b (block_begin ascends).
+__global__ __launch_bounds__(256) void k_lora_mid_small_batch(MidBatch bt) {
+  __shared__ __attribute__((aligned(16))) float lds[(kSmallR + kSmallJ) * kSmallRS];
+  const int b = (int)blockIdx.x;
+  int it = 0;
+  for (int i = 1; i < bt.count; ++i)
+    if (b >= bt.it[i].block_begin) it = i;
+  const MidItem& I = bt.it[it];
+  lora_mid_small<kSmallR, kSmallJ, kSmallKR>(I.x, I.m, I.k, I.a, I.rank, I.mid, b - I.block_begin, lds);
 }
 
 // dot_scores (tensor.rs:6-25, the x86-64 order) of a[0..len) and b[0..len)
@@ -1768,15 +1784,27 @@ hipError_t launch_linear_fp32(const FProj& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+bool lora_mid_small_ok(const float* x, int m, int k, const float* a) {
+  return k % 4 == 0 && ((size_t)x & 15) == 0 && ((size_t)a & 15) == 0 && m <= DQ8_MID_SMALL_M &&
+         ((k + 255) & ~255) <= kSmallKR;
+}
+long lora_mid_small_blocks(int m, int rank) { return (long)((m + kSmallR - 1) / kSmallR) * ((rank + kSmallJ - 1) / kSmallJ); }
+
+hipError_t launch_lora_mid_batch(const MidBatch& b, long blocks, hipStream_t s) {
+  if (b.count == 0 || blocks == 0) return hipSuccess;
+  k_lora_mid_small_batch<<<(unsigned)blocks, 256, 0, s>>>(b);
+  return hipGetLastError();
+}
+
 hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int rank, float* mid, hipStream_t s) {
   if (m == 0 || rank == 0) return hipSuccess;
   const bool dma = k % 4 == 0 && ((size_t)x & 15) == 0 && ((size_t)a & 15) == 0;
   const int kr = (k + 255) & ~255;
-  if (dma && m <= DQ8_MID_SMALL_M && kr <= 6656) {
+  if (dma && m <= DQ8_MID_SMALL_M && kr <= kSmallKR) {
     // 4 x rows and 2 adapter rows per block (6 rows in LDS: the fewest for a
     // wave of lane sums); measured 6.1 us at 24 x 2048 rank 16 against 8.4 for
     // 8 x 4 blocks and 8.2 for the tiled kernel, 14.3 against 20.8 at k = 6144
-    k_lora_mid_small<4, 2, 6656><<<(unsigned)((m + 3) / 4 * ((rank + 1) / 2)), 256, 0, s>>>(x, m, k, a, rank, mid);
+    k_lora_mid_small<<<(unsigned)lora_mid_small_blocks(m, rank), 256, 0, s>>>(x, m, k, a, rank, mid);
   } else if (dma) {
     const long blocks = (long)((m + kMidRows - 1) / kMidRows) * ((rank + kMidJ - 1) / kMidJ);
     k_lora_mid_dma<<<(unsigned)blocks, 256, 0, s>>>(x, m, k, a, rank, mid);

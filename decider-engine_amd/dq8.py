@@ -69,6 +69,17 @@ class _FfnWeights(ctypes.Structure):
     ]
 
 
+class _MidItem(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("m", ctypes.c_size_t),
+        ("k", ctypes.c_size_t),
+        ("a", ctypes.c_void_p),
+        ("rank", ctypes.c_size_t),
+        ("mid", ctypes.c_void_p),
+    ]
+
+
 class _Item(ctypes.Structure):
     _fields_ = [
         ("w", ctypes.c_void_p),
@@ -114,6 +125,7 @@ def lib() -> ctypes.CDLL:
         "dq8_linear_f32in": ([_vp, _vp, _vp, _sz, _vp, _vp, _i, _i, _vp], _i),
         "dq8_linear_batch": ([_vp, ctypes.POINTER(_Item), _sz, _vp], _i),
         "dq8_lora_mid": ([_vp, _vp, _sz, _sz, _vp, _sz, _vp, _vp], _i),
+        "dq8_lora_mid_batch": ([_vp, ctypes.POINTER(_MidItem), _sz, _vp], _i),
         "dq8_linear_lora": ([_vp, _vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
         "dq8_linear_q": ([_vp, _vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _vp, _vp, _vp, _vp], _i),
         "dq8_ffn": ([_vp, ctypes.POINTER(_FfnWeights), _vp, _vp, _sz, _vp, _vp, _vp, _vp], _i),
@@ -362,6 +374,26 @@ class Context:
         _check(lib().dq8_lora_mid(self.handle, x.data_ptr(), m, k, a.data_ptr(), rank, mid.data_ptr(),
                                   _stream(self.device)), "dq8_lora_mid")
         return mid
+
+    def lora_mid_batch(self, pairs, mids=None):
+        """dq8_lora_mid of every (x, lora_A) pair, grouped into as few launches as
+        possible; returns the middle products (the given `mids`, or new tensors)."""
+        torch = _torch()
+        arr = (_MidItem * max(1, len(pairs)))()
+        out = []
+        for i, (x, a) in enumerate(pairs):
+            self._dev(x, torch.float32, name="x")
+            self._dev(a, torch.float32, name="lora_A")
+            m, k = x.shape
+            rank, ka = a.shape
+            if ka != k:
+                raise Dq8Error(ERR_SHAPE, "dq8_lora_mid_batch: lora_A width differs from the input")
+            mid = mids[i] if mids is not None else torch.zeros((m, rank), dtype=torch.float32, device=self.device)
+            self._dev(mid, torch.float32, (m, rank), "mid")
+            arr[i] = _MidItem(x.data_ptr(), m, k, a.data_ptr(), rank, mid.data_ptr())
+            out.append(mid)
+        _check(lib().dq8_lora_mid_batch(self.handle, arr, len(pairs), _stream(self.device)), "dq8_lora_mid_batch")
+        return out
 
     def _lora(self, lora: Lora, m: int, n: int) -> _Lora:
         torch = _torch()

@@ -153,6 +153,23 @@ typedef struct dq8_lora {
  * above 2^40, or ceil(m/8) * ceil(rank/16) >= 2^23. */
 dq8_status dq8_lora_mid(dq8_ctx *ctx, const float *x, size_t m, size_t k, const float *a, size_t rank, float *mid,
                         void *stream);
+/* Several middle products (dq8_lora_mid of each item) in as few launches as
+ * possible: the projections of a question that carry adapters, each with its
+ * own input x [m][k], lora_A [rank][k] and output mid [m][rank].  Items of at
+ * most 32 rows (k % 4 == 0, x and a 16-byte aligned, k <= 6656) share grouped
+ * launches of up to 32 items; others run one launch each.  Every item is
+ * checked as dq8_lora_mid checks it before anything is enqueued; the results
+ * are those of dq8_lora_mid, bit for bit.  No reference counterpart: the crate
+ * computes each adapter's middle product in its own Linear::apply_into_shared
+ * call (weights.rs:480, 495); this only schedules those products together. */
+typedef struct {
+    const float *x;
+    size_t m, k;
+    const float *a;
+    size_t rank;
+    float *mid;
+} dq8_lora_mid_item;
+dq8_status dq8_lora_mid_batch(dq8_ctx *ctx, const dq8_lora_mid_item *items, size_t count, void *stream);
 /* dq8_linear with the projection's LoRA adapter (Projection::apply_quantized with
  * `adapter`, tensor.rs:134-183).  lora == NULL is dq8_linear. */
 dq8_status dq8_linear_lora(dq8_ctx *ctx, const dq8_weights *w, const int8_t *q, const float *scales, size_t m,

@@ -502,6 +502,44 @@ def test_lora_mid_bit_exact(ctx, m, k, rank):
     assert bits_equal(got, dq8o.lora_mid(x, a, threads=4))
 
 
+def test_lora_mid_batch_matches_single_calls(ctx):
+    # a question's adapters in one call: few-rows items share grouped launches
+    # (40 of them: two launches), the others (more rows, k % 4 != 0, unaligned
+    # x, rank 0) run on their own; every result equals its single call and the oracle
+    rng = np.random.default_rng(40)
+    shapes = [(24, 2048, 16), (24, 6144, 16), (9, 512, 8), (32, 3332, 7), (1, 64, 1)] * 7 + \
+             [(40, 256, 16), (24, 131, 5), (24, 2048, 0), (0, 2048, 16), (17, 6660, 3)]
+    pairs, wants = [], []
+    for m, k, rank in shapes:
+        x = make_x(rng, m, k)
+        a = (rng.standard_normal((rank, k)) * 0.05).astype(np.float32)
+        pairs.append((dev(x), dev(a)))
+        wants.append(dq8o.lora_mid(x, a, threads=4) if m and rank else np.zeros((m, rank), np.float32))
+    xf = torch.zeros(24 * 2048 + 1, dtype=torch.float32, device="cuda")
+    xu = xf[1:].view(24, 2048)
+    xu.copy_(pairs[0][0])
+    pairs.append((xu, pairs[0][1]))
+    wants.append(wants[0])
+    got = ctx.lora_mid_batch(pairs)
+    for (x, a), g, want in zip(pairs, got, wants):
+        assert bits_equal(host(g), want)
+        if x.shape[0] and a.shape[0]:
+            assert bits_equal(host(ctx.lora_mid(x, a)), want)
+
+
+def test_lora_mid_batch_rejects_before_running(ctx):
+    # one bad item (lora_A narrower than x): nothing is written, status SHAPE
+    good = (dev(np.ones((4, 64), np.float32)), dev(np.ones((2, 64), np.float32)))
+    mid = torch.full((4, 2), -1.0, device="cuda")
+    lib = dq8.lib()
+    arr = (dq8._MidItem * 2)()
+    arr[0] = dq8._MidItem(good[0].data_ptr(), 4, 64, good[1].data_ptr(), 2, mid.data_ptr())
+    arr[1] = dq8._MidItem(good[0].data_ptr(), 4, 0, good[1].data_ptr(), 2, mid.data_ptr())
+    assert lib.dq8_lora_mid_batch(ctx.handle, arr, 2, None) == dq8.ERR_SHAPE
+    torch.cuda.synchronize()
+    assert (host(mid) == -1.0).all()
+
+
 def same_nan(got, want):
     """Bit-equal outside NaNs, NaN at the same positions (payloads differ between x86 and the GPU)."""
     got, want = np.asarray(got), np.asarray(want)
