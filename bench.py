@@ -161,23 +161,33 @@ def main():
         return ("mid", lib.dq8_lora_mid, (ctx.handle, x.data_ptr(), M, k, a.data_ptr(), rank, mid.data_ptr(), sh),
                 (0, 2 * M * k * rank))
 
-    def lora_linear(L, name, x, q, s, out, ep, mid, k):
+    def mid_batch_call(entries):
+        """The middle products of projections that share an input, in one dq8_lora_mid_batch call:
+        entries = [(x, A, mid, k)]."""
+        arr = (dq8._MidItem * len(entries))()
+        for i, (x, a, mid, k) in enumerate(entries):
+            arr[i] = dq8._MidItem(x.data_ptr(), M, k, a.data_ptr(), rank, mid.data_ptr())
+        keep.append(arr)
+        return ("mid", lib.dq8_lora_mid_batch, (ctx.handle, arr, len(entries), sh),
+                (0, sum(2 * M * k * rank for _, _, _, k in entries)))
+
+    def lora_linear(L, name, x, q, s, out, ep, mid, k, with_mid=True):
         """mid = linear(x, A) then the projection with its adapter (weights.rs:492-520)."""
         a, b = lora_of(L, name)
         w = L[name]
         lo = dq8._Lora(mid.data_ptr(), b.data_ptr(), rank, 2.0)
         keep.append(lo)
-        return [mid_call(x, a, mid, k),
-                ("linear", lib.dq8_linear_lora, (ctx.handle, w.handle, q.data_ptr(), s.data_ptr(), M, None,
-                                                 ctypes.byref(lo), out.data_ptr(), dq8.ROWS, ep, sh),
+        return ([mid_call(x, a, mid, k)] if with_mid else []) + \
+               [("linear", lib.dq8_linear_lora, (ctx.handle, w.handle, q.data_ptr(), s.data_ptr(), M, None,
+                                                  ctypes.byref(lo), out.data_ptr(), dq8.ROWS, ep, sh),
                  (0, 2 * M * w.n * w.k))]
 
     def build(with_lora):
         calls = []
 
-        def proj(L, name, x, q, s, out, ep, mid, k):
+        def proj(L, name, x, q, s, out, ep, mid, k, with_mid=True):
             if with_lora:
-                calls.extend(lora_linear(L, name, x, q, s, out, ep, mid, k))
+                calls.extend(lora_linear(L, name, x, q, s, out, ep, mid, k, with_mid))
             else:
                 calls.append(linear(L[name], q, s, out, ep))
 
@@ -188,26 +198,32 @@ def main():
             else:
                 items = (dq8._Item * 3)()
                 outs = (mixer_out, k_out, v_out)
+                shared = []  # q, k and v share their input: one grouped launch of their middle products
                 for i, name in enumerate(("q", "k", "v")):
                     lp = None
                     if with_lora:
                         a, b = lora_of(L, name)
                         mid = torch.empty((M, rank), dtype=torch.float32, device=dev)
                         keep.append(mid)
-                        calls.append(mid_call(L["x"], a, mid, HIDDEN))
+                        shared.append((L["x"], a, mid, HIDDEN))
                         lo = dq8._Lora(mid.data_ptr(), b.data_ptr(), rank, 2.0)
                         keep.append(lo)
                         lp = ctypes.pointer(lo)
                     items[i] = dq8._Item(L[name].handle, qx.data_ptr(), sx.data_ptr(), M, None, outs[i].data_ptr(),
                                          dq8.ROWS, dq8.WRITE, lp)
                 keep.append(items)
+                if shared:
+                    calls.append(mid_batch_call(shared))
                 flops = sum(2 * M * L[n].n * L[n].k for n in ("q", "k", "v"))
                 calls.append(("linear", lib.dq8_linear_batch, (ctx.handle, items, 3, sh), (0, flops)))
             calls.append(quant(L["mix"], qx, sx, HIDDEN))
             proj(L, "out" if L["kind"] == "gdn" else "o", L["mix"], qx, sx, proj_out, dq8.WRITE, mids["a"], HIDDEN)
             calls.append(quant(L["ffn"], qx, sx, HIDDEN))
-            proj(L, "gate", L["ffn"], qx, sx, gate, dq8.WRITE, mids["b"], HIDDEN)
-            proj(L, "up", L["ffn"], qx, sx, gate, dq8.SWIGLU, mids["c"], HIDDEN)
+            if with_lora:  # gate and up share their input: one grouped launch of their middle products
+                calls.append(mid_batch_call([(L["ffn"], lora_of(L, "gate")[0], mids["b"], HIDDEN),
+                                             (L["ffn"], lora_of(L, "up")[0], mids["c"], HIDDEN)]))
+            proj(L, "gate", L["ffn"], qx, sx, gate, dq8.WRITE, mids["b"], HIDDEN, with_mid=False)
+            proj(L, "up", L["ffn"], qx, sx, gate, dq8.SWIGLU, mids["c"], HIDDEN, with_mid=False)
             calls.append(quant(gate, qf, sf, FFN_DIM))
             proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
         return calls
@@ -343,7 +359,8 @@ def main():
 def run_lora_stack(args, torch, stream, build, run_step, step_ops, base_ms):
     """The same stack with a rank-r FP32 LoRA pair on every projection, as the
     reference's checkpoints carry (weights.rs:420-424): per projection the middle
-    product mid = x.A^T (dq8_lora_mid) and the projection with its adapter."""
+    product mid = x.A^T (dq8_lora_mid; one dq8_lora_mid_batch launch for the projections
+    that share an input, q/k/v and gate/up) and the projection with its adapter."""
     calls = build(True)
     for _ in range(2):
         run_step(calls=calls)

@@ -731,29 +731,36 @@ dq8_status dq8_lora_mid_batch(dq8_ctx* ctx, const dq8_lora_mid_item* items, size
   }
   DeviceGuard guard(ctx->device);
   hipStream_t s = (hipStream_t)stream;
-  dq8::MidBatch b;
-  b.count = 0;
-  long blocks = 0;
+  // two grouped launches build up side by side: few-rows items and LDS-tiled items
+  dq8::MidBatch b[2];
+  long blocks[2] = {0, 0};
+  b[0].count = b[1].count = 0;
   for (size_t i = 0; i < count; ++i) {
     const dq8_lora_mid_item& it = items[i];
     if (it.m == 0 || it.rank == 0) continue;
     const int m = (int)it.m, k = (int)it.k, rank = (int)it.rank;
-    if (!dq8::lora_mid_small_ok(it.x, m, k, it.a)) {  // other kernels: a launch of its own
+    const bool small = dq8::lora_mid_small_ok(it.x, m, k, it.a);
+    if (!small && !dq8::lora_mid_tiled_ok(it.x, k, it.a)) {  // the plain-memory kernel: a launch of its own
       hipError_t e = dq8::launch_lora_mid(it.x, m, k, it.a, rank, it.mid, s);
       if (e != hipSuccess) return from_hip(e);
       continue;
     }
-    const long nb = dq8::lora_mid_small_blocks(m, rank);
-    if (b.count == dq8::kMaxMids || blocks + nb >= ((long)1 << 23)) {
-      hipError_t e = dq8::launch_lora_mid_batch(b, blocks, s);
+    const int t = small ? 0 : 1;
+    const long nb = small ? dq8::lora_mid_small_blocks(m, rank) : dq8::lora_mid_tiled_blocks(m, rank);
+    if (b[t].count == dq8::kMaxMids || blocks[t] + nb >= ((long)1 << 23)) {
+      hipError_t e = dq8::launch_lora_mid_batch(b[t], blocks[t], t == 1, s);
       if (e != hipSuccess) return from_hip(e);
-      b.count = 0;
-      blocks = 0;
+      b[t].count = 0;
+      blocks[t] = 0;
     }
-    b.it[b.count++] = {it.x, it.a, it.mid, m, k, rank, (int)blocks};
-    blocks += nb;
+    b[t].it[b[t].count++] = {it.x, it.a, it.mid, m, k, rank, (int)blocks[t]};
+    blocks[t] += nb;
   }
-  return from_hip(dq8::launch_lora_mid_batch(b, blocks, s));
+  for (int t = 0; t < 2; ++t) {
+    hipError_t e = dq8::launch_lora_mid_batch(b[t], blocks[t], t == 1, s);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  return DQ8_OK;
 }
 
 dq8_status dq8_linear_batch(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, void* stream) {

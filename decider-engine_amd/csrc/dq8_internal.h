@@ -62,7 +62,7 @@ struct Batch {
 };
 
 // LoRA middle products of several (x, A) pairs in one launch of the few-rows
-// kernel (lora_mid_small_ok items only).
+// kernel (lora_mid_small_ok items) or of the LDS-tiled kernel.
 struct MidItem {
   const float* x;
   const float* a;
@@ -113,7 +113,9 @@ hipError_t launch_linear_fp32(const FProj& p, hipStream_t s);
 hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int rank, float* mid, hipStream_t s);
 bool lora_mid_small_ok(const float* x, int m, int k, const float* a);  // the few-rows kernel takes it
 long lora_mid_small_blocks(int m, int rank);
-hipError_t launch_lora_mid_batch(const MidBatch& b, long blocks, hipStream_t s);
+bool lora_mid_tiled_ok(const float* x, int k, const float* a);  // otherwise the LDS-tiled kernel, if this holds
+long lora_mid_tiled_blocks(int m, int rank);
+hipError_t launch_lora_mid_batch(const MidBatch& b, long blocks, bool tiled, hipStream_t s);
 // Kind: 0 wide (M > 32), 1 skinny (M <= 16), 2 skinny (16 < M <= 32).  dots
 // selects the debug kernel.
 constexpr int kKinds = 3;

@@ -1475,14 +1475,14 @@ constexpr int kMidRows = 8, kMidJ = 16, kMidKT = 256, kMidStride = kMidKT + 8;
 #endif
 constexpr int kMidSlots = DQ8_MID_SLOTS, kMidLoads = 6;  // DMA loads per wave per tile
 constexpr int kMidBatch = DQ8_MID_BATCH;
-__global__ __launch_bounds__(256) void k_lora_mid_dma(const float* __restrict__ x, int m, int k,
-                                                      const float* __restrict__ a, int rank, float* __restrict__ mid) {
+typedef float MidTile[kMidSlots][kMidRows + kMidJ][kMidStride];
+__device__ __forceinline__ void lora_mid_tiled(const float* __restrict__ x, int m, int k, const float* __restrict__ a,
+                                               int rank, float* __restrict__ mid, int block, MidTile& lds) {
   typedef float f32x4 __attribute__((ext_vector_type(4)));
-  __shared__ __attribute__((aligned(16))) float lds[kMidSlots][kMidRows + kMidJ][kMidStride];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int jblocks = (rank + kMidJ - 1) / kMidJ;
-  const int r0 = (int)(blockIdx.x / jblocks) * kMidRows, j0 = (int)(blockIdx.x % jblocks) * kMidJ;
+  const int r0 = (block / jblocks) * kMidRows, j0 = (block % jblocks) * kMidJ;
   const int chunks = k >> 3, full = 8 * chunks;
   const int tiles = (full + kMidKT - 1) / kMidKT;
   const float* xrow[2];
@@ -1564,6 +1564,22 @@ __global__ __launch_bounds__(256) void k_lora_mid_dma(const float* __restrict__ 
       mid[(size_t)row * rank + j] = sum + 0.0f;
     }
   }
+}
+__global__ __launch_bounds__(256) void k_lora_mid_dma(const float* __restrict__ x, int m, int k,
+                                                      const float* __restrict__ a, int rank, float* __restrict__ mid) {
+  __shared__ __attribute__((aligned(16))) MidTile lds;
+  lora_mid_tiled(x, m, k, a, rank, mid, (int)blockIdx.x, lds);
+}
+// Several tiled middle products in one launch (block -> item as in
+// k_lora_mid_small_batch).
+__global__ __launch_bounds__(256) void k_lora_mid_dma_batch(MidBatch bt) {
+  __shared__ __attribute__((aligned(16))) MidTile lds;
+  const int b = (int)blockIdx.x;
+  int it = 0;
+  for (int i = 1; i < bt.count; ++i)
+    if (b >= bt.it[i].block_begin) it = i;
+  const MidItem& I = bt.it[it];
+  lora_mid_tiled(I.x, I.m, I.k, I.a, I.rank, I.mid, b - I.block_begin, lds);
 }
 
 // k_lora_mid_small<R, J>: few rows (m <= 32).  A block holds R whole rows of x
@@ -1790,9 +1806,19 @@ bool lora_mid_small_ok(const float* x, int m, int k, const float* a) {
 }
 long lora_mid_small_blocks(int m, int rank) { return (long)((m + kSmallR - 1) / kSmallR) * ((rank + kSmallJ - 1) / kSmallJ); }
 
-hipError_t launch_lora_mid_batch(const MidBatch& b, long blocks, hipStream_t s) {
+bool lora_mid_tiled_ok(const float* x, int k, const float* a) {
+  return k % 4 == 0 && ((size_t)x & 15) == 0 && ((size_t)a & 15) == 0;
+}
+long lora_mid_tiled_blocks(int m, int rank) {
+  return (long)((m + kMidRows - 1) / kMidRows) * ((rank + kMidJ - 1) / kMidJ);
+}
+
+hipError_t launch_lora_mid_batch(const MidBatch& b, long blocks, bool tiled, hipStream_t s) {
   if (b.count == 0 || blocks == 0) return hipSuccess;
-  k_lora_mid_small_batch<<<(unsigned)blocks, 256, 0, s>>>(b);
+  if (tiled)
+    k_lora_mid_dma_batch<<<(unsigned)blocks, 256, 0, s>>>(b);
+  else
+    k_lora_mid_small_batch<<<(unsigned)blocks, 256, 0, s>>>(b);
   return hipGetLastError();
 }
 

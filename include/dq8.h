@@ -155,9 +155,10 @@ dq8_status dq8_lora_mid(dq8_ctx *ctx, const float *x, size_t m, size_t k, const 
                         void *stream);
 /* Several middle products (dq8_lora_mid of each item) in as few launches as
  * possible: the projections of a question that carry adapters, each with its
- * own input x [m][k], lora_A [rank][k] and output mid [m][rank].  Items of at
- * most 32 rows (k % 4 == 0, x and a 16-byte aligned, k <= 6656) share grouped
- * launches of up to 32 items; others run one launch each.  Every item is
+ * own input x [m][k], lora_A [rank][k] and output mid [m][rank].  Items with
+ * k % 4 == 0 and 16-byte aligned x and a share grouped launches of up to 32
+ * items (one for items of at most 32 rows and k <= 6656, one for the others);
+ * the rest run one launch each.  Every item is
  * checked as dq8_lora_mid checks it before anything is enqueued; the results
  * are those of dq8_lora_mid, bit for bit.  No reference counterpart: the crate
  * computes each adapter's middle product in its own Linear::apply_into_shared

@@ -503,12 +503,14 @@ def test_lora_mid_bit_exact(ctx, m, k, rank):
 
 
 def test_lora_mid_batch_matches_single_calls(ctx):
-    # a question's adapters in one call: few-rows items share grouped launches
-    # (40 of them: two launches), the others (more rows, k % 4 != 0, unaligned
-    # x, rank 0) run on their own; every result equals its single call and the oracle
+    # adapters in one call: few-rows items share grouped launches (35 of them:
+    # two launches), items with more rows or k > 6656 share grouped launches of
+    # the tiled kernel, the rest (k % 4 != 0, unaligned x) run on their own and
+    # rank 0 / m 0 do nothing; every result equals its single call and the oracle
     rng = np.random.default_rng(40)
     shapes = [(24, 2048, 16), (24, 6144, 16), (9, 512, 8), (32, 3332, 7), (1, 64, 1)] * 7 + \
-             [(40, 256, 16), (24, 131, 5), (24, 2048, 0), (0, 2048, 16), (17, 6660, 3)]
+             [(40, 256, 16), (24, 131, 5), (24, 2048, 0), (0, 2048, 16), (17, 6660, 3), (130, 2048, 16),
+              (64, 6144, 40), (2048, 2048, 16)]
     pairs, wants = [], []
     for m, k, rank in shapes:
         x = make_x(rng, m, k)
