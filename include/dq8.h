@@ -160,7 +160,8 @@ dq8_status dq8_lora_mid(dq8_ctx *ctx, const float *x, size_t m, size_t k, const 
  * items (one for items of at most 32 rows and k <= 6656, one for the others);
  * the rest run one launch each.  Every item is
  * checked as dq8_lora_mid checks it before anything is enqueued; the results
- * are those of dq8_lora_mid, bit for bit.  No reference counterpart: the crate
+ * are those of dq8_lora_mid, bit for bit.  Items run concurrently: no item's
+ * mid may overlap another item's x, a or mid.  No reference counterpart: the crate
  * computes each adapter's middle product in its own Linear::apply_into_shared
  * call (weights.rs:480, 495); this only schedules those products together. */
 typedef struct {
