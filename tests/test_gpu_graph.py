@@ -1,9 +1,9 @@
 """HIP graph capture of the library's asynchronous calls.
 
 A step of quantize / linear (wide and skinny) / grouped launch / SwiGlu / Add /
-LoRA / FFN chain / apply (device-side path choice) is captured once on a side
-stream and replayed several times, with eager work and synchronizations in
-between.  Every replay must reproduce the eager results bit for bit (NaN
+LoRA (single and grouped middle products) / FFN chain / apply (device-side path
+choice) is captured once on a side stream and replayed several times, with eager
+work and synchronizations in between.  Every replay must reproduce the eager results bit for bit (NaN
 positions for the non-finite apply)."""
 import numpy as np
 import pytest
@@ -41,6 +41,7 @@ def test_captured_step_replays_bit_exact(ctx):
     qs = torch.empty((24, H), dtype=torch.int8, device="cuda")
     ss = torch.empty((24, H // 64), dtype=torch.float32, device="cuda")
     mid = torch.empty((M, 8), dtype=torch.float32, device="cuda")
+    x24 = dev(rng.standard_normal((24, H)).astype(np.float32))
 
     def step(o):
         """Writes every result into the dict of buffers o."""
@@ -51,6 +52,7 @@ def test_captured_step_replays_bit_exact(ctx):
         ctx.linear(wq, qs, ss, out=o["skinny"])
         ctx.linear_batch([dq8.Item(wg, q, s, o["g1"]), dq8.Item(wg, qs, ss, o["g2"])])
         ctx.lora_mid(x, A, mid=mid)
+        ctx.lora_mid_batch([(x, A), (x24, A), (xs, A)], mids=[o["mb0"], o["mb1"], o["mb2"]])
         ctx.linear_lora(wg, q, s, dq8.Lora(mid, B, 0.5), out=o["lora"])
         ctx.ffn(wg, wu, wd, q, s, o["res"], h=o["h"])
         ctx.apply(wq, xn, out=o["apply"])
@@ -58,7 +60,7 @@ def test_captured_step_replays_bit_exact(ctx):
     def buffers():
         z = lambda *shape: torch.zeros(shape, dtype=torch.float32, device="cuda")
         return {"res": z(M, H), "wide": z(M, H), "skinny": z(24, H), "g1": z(M, F), "g2": z(24, F),
-                "lora": z(M, F), "h": z(M, F), "apply": z(M, H)}
+                "lora": z(M, F), "h": z(M, F), "apply": z(M, H), "mb0": z(M, 8), "mb1": z(24, 8), "mb2": z(24, 8)}
 
     stream = torch.cuda.Stream()
     eager, graph_out = buffers(), buffers()
