@@ -7,6 +7,7 @@
 #include <new>
 #include <stdint.h>
 #include <string.h>
+#include <vector>
 
 struct dq8_ctx {
   int device;
@@ -29,6 +30,9 @@ struct dq8_ctx {
   size_t load_raw_bytes = 0;
   void* load_tmp = nullptr;
   size_t load_tmp_bytes = 0;
+  // Device buffers that were outgrown.  A graph captured earlier may still
+  // reference them, so they are freed only by dq8_destroy.
+  std::vector<void*> retired;
 };
 
 struct dq8_weights {
@@ -62,23 +66,38 @@ dq8_status from_hip(hipError_t e) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
-dq8_status ensure_buffer(void*& buf, size_t& have, size_t bytes) {
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
+// Grow a context buffer to at least `bytes`.  Never while `s` is being
+// captured (DQ8_ERR_CAPTURE: nothing is allocated or enqueued).  The old
+// buffer is retired, not freed: work queued earlier, or a graph captured
+// earlier, may still use it, so it lives until dq8_destroy.  Growth doubles,
+// so the retired buffers together stay smaller than the current one.
+dq8_status ensure_buffer(dq8_ctx* ctx, void*& buf, size_t& have, size_t bytes, hipStream_t s) {
   if (bytes <= have) return DQ8_OK;
-  if (buf) {
-    // Earlier work queued on any stream may still read the old buffer.
-    hipError_t e = hipDeviceSynchronize();
-    if (e != hipSuccess) return from_hip(e);
-    (void)hipFree(buf);
-    buf = nullptr;
-    have = 0;
-  }
-  size_t want = bytes + (bytes >> 2);
-  hipError_t e = hipMalloc(&buf, want);
+  if (capturing(s)) return DQ8_ERR_CAPTURE;
+  const size_t want = std::max(bytes, 2 * have);
+  void* fresh = nullptr;
+  hipError_t e = hipMalloc(&fresh, want);
   if (e != hipSuccess) return from_hip(e);
+  if (buf) {
+    try {
+      ctx->retired.push_back(buf);
+    } catch (...) {
+      (void)hipFree(fresh);
+      return DQ8_ERR_NOMEM;
+    }
+  }
+  buf = fresh;
   have = want;
   return DQ8_OK;
 }
-dq8_status ensure_work(dq8_ctx* ctx, size_t bytes) { return ensure_buffer(ctx->work, ctx->work_bytes, bytes); }
+dq8_status ensure_work(dq8_ctx* ctx, size_t bytes, hipStream_t s) {
+  return ensure_buffer(ctx, ctx->work, ctx->work_bytes, bytes, s);
+}
 
 dq8_status make_weights(dq8_ctx* ctx, size_t n, size_t k, dq8_weights** out) {
   if (n == 0 || k == 0 || n > (1u << 30) || k > (1u << 30) || n * k > ((size_t)1 << 40)) return DQ8_ERR_SHAPE;
@@ -237,7 +256,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
       need += xs_pad_bytes(items[i].w->w, items[i].m);
   }
   if (need) {
-    dq8_status st = ensure_work(ctx, need);
+    dq8_status st = ensure_work(ctx, need, s);
     if (st != DQ8_OK) return st;
   }
   dq8::Batch batch[dq8::kKinds];
@@ -344,6 +363,14 @@ dq8_status check_f32in(const dq8_ctx* ctx, const dq8_weights* w, const float* x,
   return check_lora(lora);
 }
 
+// Workspace of dq8_ffn for m rows of intermediate width inter and a down
+// adapter of rank `rank`: q_h [m][inter], scales_h [m][G] (16-byte aligned),
+// the down adapter's middle product [m][rank].
+size_t chain_bytes(size_t m, size_t inter, size_t rank) {
+  const size_t gh = (inter + kGroup - 1) / kGroup;
+  return (m * inter + 255) / 256 * 256 + (m * gh * sizeof(float) + 255) / 256 * 256 + m * rank * sizeof(float);
+}
+
 // Inputs quantized into the context workspace: q with rows of G*64 bytes,
 // scales with rows of a multiple of 4 groups.
 struct WorkInputs {
@@ -353,21 +380,37 @@ struct WorkInputs {
   int ldxs;
 };
 
-// QuantizedInputs::new of x [m][w.k] into the workspace.  ctx->flag is
-// cleared first and ends up non-zero if x holds a non-finite value.
+// Bytes of quantized inputs (rows of G*64 bytes) for m rows, and where the
+// scales (rows of a multiple of 4 groups) start after them.
+size_t work_q_bytes(const dq8::Weights& w, size_t m) { return (m * (size_t)w.g * kGroup + 255) / 256 * 256; }
+
+// Inputs laid out at base: q, then the scales.
+WorkInputs inputs_at(const dq8::Weights& w, size_t m, void* base) {
+  WorkInputs in;
+  in.q = (int8_t*)base;
+  in.ldq = w.g * kGroup;
+  in.xs = (float*)((char*)base + work_q_bytes(w, m));
+  in.ldxs = padded_groups(w);
+  return in;
+}
+
+// QuantizedInputs::new of x [m][w.k] into `in`.  *flag is cleared first (by a
+// kernel, so the call can be graph-captured) and ends up non-zero if x holds
+// a non-finite value.
+dq8_status quantize_into(const dq8::Weights& w, const float* x, size_t m, const WorkInputs& in, uint32_t* flag,
+                         hipStream_t s) {
+  hipError_t e = dq8::launch_fill_u32(flag, 0, s);
+  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, w.k, in.q, in.ldq, in.xs, in.ldxs, flag, s);
+  return from_hip(e);
+}
+
+// The same into the context workspace, with ctx->flag.
 dq8_status quantize_to_work(dq8_ctx* ctx, const dq8::Weights& w, const float* x, size_t m, hipStream_t s,
                             WorkInputs& in) {
-  const size_t ldq = (size_t)w.g * kGroup;
-  const size_t qbytes = (m * ldq + 255) / 256 * 256;
-  dq8_status st = ensure_work(ctx, qbytes + xs_pad_bytes(w, m));
+  dq8_status st = ensure_work(ctx, work_q_bytes(w, m) + xs_pad_bytes(w, m), s);
   if (st != DQ8_OK) return st;
-  in.q = (int8_t*)ctx->work;
-  in.ldq = (int)ldq;
-  in.xs = (float*)((char*)ctx->work + qbytes);
-  in.ldxs = padded_groups(w);
-  hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
-  if (e == hipSuccess) e = dq8::launch_quantize(x, (int)m, w.k, in.q, in.ldq, in.xs, in.ldxs, ctx->flag, s);
-  return from_hip(e);
+  in = inputs_at(w, m, ctx->work);
+  return quantize_into(w, x, m, in, ctx->flag, s);
 }
 
 // Waits for the stream and reports ctx->flag as DQ8_ERR_NONFINITE.
@@ -419,6 +462,17 @@ dq8::FProj make_fproj(const dq8::Weights& w, const float* x, size_t m, const flo
   return p;
 }
 
+// Projection::apply_quantized after the quantization of x into `in` with its
+// non-finite flag: both paths are queued and the flag lets exactly one of them
+// run on the device (tensor.rs:190-201), with no synchronization.
+dq8_status apply_paths(const dq8::Weights& w, const float* x, size_t m, const float* bias, const dq8_lora* lora,
+                       float* out, int layout, int epilogue, const WorkInputs& in, const uint32_t* flag,
+                       hipStream_t s) {
+  dq8_status st = launch_one(w, in, m, bias, lora, out, layout, epilogue, flag, s);
+  if (st != DQ8_OK) return st;
+  return from_hip(dq8::launch_linear_fp32(make_fproj(w, x, m, bias, lora, out, layout, epilogue, flag), s));
+}
+
 // ------------------------------------------------------------- weight loads
 
 constexpr size_t kStagingBytes = 8u << 20;
@@ -463,7 +517,7 @@ dq8_status quantize_raw_weights(dq8_ctx* ctx, const void* raw, int dtype, size_t
                                 dq8_weights** out) {
   const size_t g = groups_of(k);
   const size_t vbytes = (n * k + 255) & ~(size_t)255;
-  dq8_status st = ensure_buffer(ctx->load_tmp, ctx->load_tmp_bytes, vbytes + n * g * sizeof(float));
+  dq8_status st = ensure_buffer(ctx, ctx->load_tmp, ctx->load_tmp_bytes, vbytes + n * g * sizeof(float), s);
   if (st != DQ8_OK) return st;
   uint8_t* values = static_cast<uint8_t*>(ctx->load_tmp);
   float* scales = reinterpret_cast<float*>(values + vbytes);
@@ -485,7 +539,7 @@ dq8_status quantize_raw_weights(dq8_ctx* ctx, const void* raw, int dtype, size_t
 template <typename Fill>
 dq8_status load_weights(dq8_ctx* ctx, int dtype, size_t n, size_t k, hipStream_t s, dq8_weights** out, Fill fill) {
   const size_t bytes = n * k * raw_element_bytes(dtype);
-  dq8_status st = ensure_buffer(ctx->load_raw, ctx->load_raw_bytes, bytes);
+  dq8_status st = ensure_buffer(ctx, ctx->load_raw, ctx->load_raw_bytes, bytes, s);
   if (st != DQ8_OK) return st;
   uint8_t* raw = static_cast<uint8_t*>(ctx->load_raw);
   st = stage_to_device(ctx, raw, bytes, s, fill);
@@ -510,6 +564,7 @@ const char* dq8_status_string(dq8_status s) {
     case DQ8_ERR_NOMEM: return "out of device memory";
     case DQ8_ERR_FORMAT: return "invalid safetensors data";
     case DQ8_ERR_IO: return "file read failed";
+    case DQ8_ERR_CAPTURE: return "the call would allocate while its stream is being captured";
   }
   return "unknown status";
 }
@@ -546,8 +601,24 @@ dq8_status dq8_destroy(dq8_ctx* ctx) {
   }
   (void)hipFree(ctx->load_raw);
   (void)hipFree(ctx->load_tmp);
+  for (void* p : ctx->retired) (void)hipFree(p);
   delete ctx;
   return DQ8_OK;
+}
+
+dq8_status dq8_reserve(dq8_ctx* ctx, size_t m, size_t k, size_t rank) {
+  if (!ctx) return DQ8_ERR_ARG;
+  if (m > (1u << 30) || k > (1u << 30) || rank > (1u << 20) || m * k > ((size_t)1 << 40)) return DQ8_ERR_SHAPE;
+  if (m == 0 || k == 0) return DQ8_OK;
+  DeviceGuard guard(ctx->device);
+  // the largest workspace of one projection with K <= k: quantized rows of
+  // G*64 bytes plus scales rows of a multiple of 4 groups (dq8_apply,
+  // dq8_linear_f32in), which also covers the padded copies of dq8_linear
+  const size_t g = groups_of(k), gp = (g + 3) / 4 * 4;
+  const size_t work = (m * g * kGroup + 255) / 256 * 256 + (m * gp * sizeof(float) + 255) / 256 * 256;
+  dq8_status st = ensure_work(ctx, work, nullptr);
+  if (st == DQ8_OK) st = ensure_buffer(ctx, ctx->chain, ctx->chain_bytes, chain_bytes(m, k, rank), nullptr);
+  return st;
 }
 
 dq8_status dq8_weights_from_quantized(dq8_ctx* ctx, const uint8_t* values, const float* scales, size_t n, size_t k,
@@ -572,23 +643,12 @@ dq8_status dq8_weights_from_quantized(dq8_ctx* ctx, const uint8_t* values, const
 dq8_status dq8_weights_from_f32(dq8_ctx* ctx, const float* w, size_t n, size_t k, void* stream, dq8_weights** out) {
   if (!ctx || !w || !out) return DQ8_ERR_ARG;
   *out = nullptr;
-  if (n == 0 || k == 0 || n > (1u << 30) || k > (1u << 30)) return DQ8_ERR_SHAPE;
+  if (!raw_shape_ok(n, k)) return DQ8_ERR_SHAPE;
   DeviceGuard guard(ctx->device);
-  hipStream_t s = (hipStream_t)stream;
-  const size_t g = groups_of(k);
-  uint8_t* values = nullptr;
-  float* scales = nullptr;
-  hipError_t e = hipMalloc(&values, n * k);
-  if (e == hipSuccess) e = hipMalloc(&scales, n * g * sizeof(float));
-  // Data::quantize has the same per-group formula as QuantizedInputs::new (weights.rs:117-136).
-  if (e == hipSuccess)
-    e = dq8::launch_quantize(w, (int)n, (int)k, (int8_t*)values, (int)k, scales, (int)groups_of(k), nullptr, s);
-  dq8_status st = from_hip(e);
-  if (st == DQ8_OK) st = dq8_weights_from_quantized(ctx, values, scales, n, k, stream, out);
-  (void)hipStreamSynchronize(s);
-  (void)hipFree(values);
-  (void)hipFree(scales);
-  return st;
+  // Data::quantize has the same per-group formula as QuantizedInputs::new
+  // (weights.rs:117-136); F32 elements decode to themselves, and non-finite
+  // weights are rejected as the crate's loader rejects them (weights.rs:170-187).
+  return quantize_raw_weights(ctx, w, dq8::kDtypeF32, n, k, (hipStream_t)stream, out);
 }
 
 dq8_status dq8_weights_from_raw(dq8_ctx* ctx, const void* data, dq8_dtype dtype, size_t n, size_t k, void* stream,
@@ -812,12 +872,9 @@ dq8_status dq8_apply(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t 
   WorkInputs in;
   st = quantize_to_work(ctx, w->w, x, m, s, in);
   if (st != DQ8_OK) return st;
-  // Both paths are queued; the device flag of the quantization lets exactly
-  // one of them run (tensor.rs:190-201), with no synchronization.
-  st = launch_one(w->w, in, m, bias, lora, out, layout, epilogue, ctx->flag, s);
-  if (st != DQ8_OK) return st;
-  return from_hip(dq8::launch_linear_fp32(make_fproj(w->w, x, m, bias, lora, out, layout, epilogue, ctx->flag), s));
+  return apply_paths(w->w, x, m, bias, lora, out, layout, epilogue, in, ctx->flag, s);
 }
+
 
 dq8_status dq8_linear_q(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, const float* scales, size_t m,
                         const float* bias, const dq8_lora* lora, float* out, dq8_epilogue epilogue, int8_t* q_out,
@@ -861,7 +918,8 @@ dq8_status dq8_ffn(dq8_ctx* ctx, const dq8_ffn_weights* f, const int8_t* q, cons
   // chain workspace: q_h [m][inter], scales_h [m][G] (16-byte aligned), down mid [m][rank]
   const size_t inter = (size_t)u.n, gh = (inter + kGroup - 1) / kGroup;
   const size_t qbytes = (m * inter + 255) / 256 * 256, sbytes = (m * gh * sizeof(float) + 255) / 256 * 256;
-  st = ensure_buffer(ctx->chain, ctx->chain_bytes, qbytes + sbytes + m * rank * sizeof(float));
+  (void)gh;
+  st = ensure_buffer(ctx, ctx->chain, ctx->chain_bytes, chain_bytes(m, inter, rank), s);
   if (st != DQ8_OK) return st;
   int8_t* qh = (int8_t*)ctx->chain;
   float* sh = (float*)((char*)ctx->chain + qbytes);

@@ -26,7 +26,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libdq8.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "dq8.h")
 
-OK, ERR_SHAPE, ERR_NONFINITE, ERR_ARG, ERR_DEVICE, ERR_NOMEM, ERR_FORMAT, ERR_IO = range(8)
+OK, ERR_SHAPE, ERR_NONFINITE, ERR_ARG, ERR_DEVICE, ERR_NOMEM, ERR_FORMAT, ERR_IO, ERR_CAPTURE = range(9)
 F32, BF16, F16 = 0, 1, 2  # dq8_dtype
 WRITE, ADD, SWIGLU = 0, 1, 2
 ROWS, COLUMNS = 0, 1
@@ -115,6 +115,7 @@ def lib() -> ctypes.CDLL:
     sig = {
         "dq8_create": ([_i, ctypes.POINTER(_vp)], _i),
         "dq8_destroy": ([_vp], _i),
+        "dq8_reserve": ([_vp, _sz, _sz, _sz], _i),
         "dq8_weights_from_f32": ([_vp, _vp, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
         "dq8_weights_from_quantized": ([_vp, _vp, _vp, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
         "dq8_weights_export": ([_vp, _vp, _vp, _vp, _vp], _i),
@@ -252,6 +253,12 @@ class Context:
         h = ctypes.c_void_p()
         _check(lib().dq8_create(device, ctypes.byref(h)), "dq8_create")
         self.handle = h.value
+
+    def reserve(self, m: int, k: int, rank: int = 0) -> None:
+        """Pre-size the context workspace for calls of up to m rows of width k
+        (and an FFN down adapter of rank `rank`), so that later calls can be
+        graph-captured without growing it."""
+        _check(lib().dq8_reserve(self.handle, m, k, rank), "dq8_reserve")
 
     def close(self) -> None:
         if getattr(self, "handle", None):
@@ -578,6 +585,12 @@ class SafeTensors:
             self.tensors.append((name.value.decode(), dt.value.decode(), tuple(shp[j] for j in range(nd.value)),
                                  nb.value))
         self._index = {t[0]: i for i, t in enumerate(self.tensors)}
+
+    def reserve(self, m: int, k: int, rank: int = 0) -> None:
+        """Pre-size the context workspace for calls of up to m rows of width k
+        (and an FFN down adapter of rank `rank`), so that later calls can be
+        graph-captured without growing it."""
+        _check(lib().dq8_reserve(self.handle, m, k, rank), "dq8_reserve")
 
     def close(self) -> None:
         if getattr(self, "handle", None):

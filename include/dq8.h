@@ -16,7 +16,22 @@
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
  *     Weight handles are immutable after creation, so calls on different
  *     streams may share them.  One context must not be used by two host
- *     threads at once (its workspace is shared by its calls).
+ *     threads at once, and its calls must be stream-ordered: the context's
+ *     workspace and non-finite flag are single device buffers, so two calls of
+ *     one context that use them (dq8_apply, dq8_linear_f32in, dq8_ffn,
+ *     dq8_linear_q, dq8_quantize with nonfinite == NULL, and any projection
+ *     whose q is not 16-byte aligned, whose k % 64 != 0 or whose scales rows
+ *     are not 16-byte aligned with ceil(k/64) % 4 == 0) must not run
+ *     concurrently on different streams.  Use one context per stream for
+ *     concurrent work.
+ *   - Graph capture: a call never allocates, frees or synchronizes while its
+ *     stream is being captured.  If it would have to grow the context
+ *     workspace it returns DQ8_ERR_CAPTURE and enqueues nothing; size the
+ *     workspace first with dq8_reserve (or run the call once eagerly at the
+ *     largest size).  A workspace that is outgrown is kept, not freed, until
+ *     dq8_destroy, so graphs captured earlier stay valid.  Calls that
+ *     synchronize by design (weight creation and loads, dq8_quantize /
+ *     dq8_linear_q with nonfinite == NULL, dq8_linear_f32in) cannot be captured.
  *   - The library starts no threads.
  *   - Weight loads keep their device buffers (stored elements, and values and
  *     scales before the repack) in the context, grown to the largest tensor
@@ -47,7 +62,8 @@ typedef enum dq8_status {
     DQ8_ERR_DEVICE = 4,    /* a HIP call failed */
     DQ8_ERR_NOMEM = 5,     /* device allocation failed */
     DQ8_ERR_FORMAT = 6,    /* a safetensors file or tensor that read_tensors / Data::read rejects */
-    DQ8_ERR_IO = 7         /* a file could not be opened or read */
+    DQ8_ERR_IO = 7,        /* a file could not be opened or read */
+    DQ8_ERR_CAPTURE = 8    /* the stream is being captured and the call would allocate (see dq8_reserve) */
 } dq8_status;
 
 /* Stored element types of weights (Data::{F32, Bf16, F16}, weights.rs:12-15),
@@ -68,12 +84,22 @@ typedef struct dq8_weights dq8_weights;
  * (Kernel::detect, int8.rs:25-30, and the rayon pool). */
 dq8_status dq8_create(int device, dq8_ctx **out);
 dq8_status dq8_destroy(dq8_ctx *ctx);
+/* Grow the context workspace, if needed, for calls of up to m rows of width
+ * k: dq8_apply / dq8_linear_f32in / a padded dq8_linear of one projection with
+ * K <= k, and dq8_ffn with an intermediate width <= k and a down adapter of
+ * rank <= rank.  A dq8_linear_batch whose items need padding needs the sum of
+ * their sizes.  Not capturable (it may allocate); no counterpart in the crate,
+ * whose Vec buffers are allocated per call. */
+dq8_status dq8_reserve(dq8_ctx *ctx, size_t m, size_t k, size_t rank);
 
 /* Data::quantize(width, Precision::Int8Compute) (weights.rs:98-146) on the device,
  * from fp32 weights w [n][k], followed by the one-time repack into the
- * MFMA fragment layout.  Synchronous with respect to `stream` on return of
- * the handle (the handle is usable by later work on any stream once `stream`
- * has progressed past this call; dq8_weights_* calls synchronize `stream`). */
+ * MFMA fragment layout.  A non-finite element returns DQ8_ERR_NONFINITE and
+ * no handle, as the crate's loader rejects such weights before quantizing
+ * them (Data::read, weights.rs:170-187).  Synchronous with respect to
+ * `stream` on return of the handle (the handle is usable by later work on any
+ * stream once `stream` has progressed past this call; dq8_weights_* calls
+ * synchronize `stream`). */
 dq8_status dq8_weights_from_f32(dq8_ctx *ctx, const float *w, size_t n, size_t k, void *stream,
                                 dq8_weights **out);
 

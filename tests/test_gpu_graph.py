@@ -19,6 +19,16 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def bits_equal(a, b):
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    return a.shape == b.shape and a.tobytes() == b.tobytes()
+
+
 def test_captured_step_replays_bit_exact(ctx):
     rng = np.random.default_rng(77)
     M, H, F = 130, 256, 384
@@ -92,3 +102,70 @@ def test_captured_step_replays_bit_exact(ctx):
         with torch.cuda.stream(stream):
             step(eager)
         torch.cuda.synchronize()
+
+
+def test_capture_does_not_grow_and_earlier_graphs_survive_growth():
+    # A fresh context has no workspace: a captured dq8_apply that would have
+    # to allocate one returns CAPTURE and enqueues nothing.  After dq8_reserve
+    # the same calls capture; an eager call at a larger size then grows the
+    # workspace, and the earlier graph (which holds the old buffer) still
+    # replays bit-exact, because outgrown buffers are kept until destroy.
+    rng = np.random.default_rng(91)
+    c = dq8.Context(0)
+    try:
+        H, F = 256, 384
+        mk = lambda n, k: (lambda v, s: (v, s, c.weights_from_quantized(dev(v), dev(s))))(
+            *dq8o.quantize_weights((rng.standard_normal((n, k)) * 0.05).astype(np.float32)))
+        wq, wg, wu, wd = mk(H, H), mk(F, H), mk(F, H), mk(H, F)
+        x0 = rng.standard_normal((24, H)).astype(np.float32)
+        res0 = rng.standard_normal((24, H)).astype(np.float32)
+        x, res_init = dev(x0), dev(res0)
+        q = torch.empty((24, H), dtype=torch.int8, device="cuda")
+        s = torch.empty((24, H // 64), dtype=torch.float32, device="cuda")
+        flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+        out = torch.zeros((24, H), dtype=torch.float32, device="cuda")
+        res = torch.zeros((24, H), dtype=torch.float32, device="cuda")
+        h = torch.zeros((24, F), dtype=torch.float32, device="cuda")
+        stream = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with pytest.raises(dq8.Dq8Error) as err:
+            with torch.cuda.graph(g, stream=stream):
+                c.apply(wq[2], x, out=out)
+        assert err.value.status == dq8.ERR_CAPTURE
+        torch.cuda.synchronize()
+        c.reserve(24, F)
+
+        def step():
+            res.copy_(res_init)
+            c.apply(wq[2], x, out=out)
+            c.quantize(x, q, s, nonfinite=flag)
+            c.ffn(wg[2], wu[2], wd[2], q, s, res, h=h)
+
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            step()
+        want_out = dq8o.linear(x0, wq[0], wq[1], threads=4)
+        gate = dq8o.linear(x0, wg[0], wg[1], threads=4)
+        want_h = dq8o.linear(x0, wu[0], wu[1], result=gate, epilogue=2, threads=4)
+        want_res = dq8o.linear(want_h, wd[0], wd[1], result=res0, epilogue=1, threads=4)
+        big = rng.standard_normal((512, H)).astype(np.float32)
+        for replay in range(3):
+            out.fill_(-1.0)
+            h.fill_(-1.0)
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert bits_equal(host(out), want_out), replay
+            assert bits_equal(host(h), want_h), replay
+            assert bits_equal(host(res), want_res), replay
+            # eager calls at a larger size grow the workspace between replays
+            got = c.apply(wq[2], dev(big))
+            assert bits_equal(host(got), dq8o.linear(big, wq[0], wq[1], threads=4)), replay
+            qb, sb = c.quantize(dev(big))
+            c.ffn(wg[2], wu[2], wd[2], qb, sb, torch.zeros((big.shape[0], H), dtype=torch.float32, device="cuda"))
+            torch.cuda.synchronize()
+            big = rng.standard_normal((512 * (replay + 2), H)).astype(np.float32)
+        del g
+    finally:
+        torch.cuda.synchronize()
+        c.close()
