@@ -4,10 +4,19 @@
 #include "dq8_st.h"
 
 #include <algorithm>
+#include <mutex>
 #include <new>
 #include <stdint.h>
 #include <string.h>
 #include <vector>
+
+// Scratch of dq8_apply_noalloc: its non-finite flag (first 256 bytes), then
+// the quantized inputs and their scales.  Each device holds its own copy for
+// the life of the process; host code uses only the per-device address that
+// hipGetSymbolAddress returns (dq8_create looks it up once per device).
+constexpr size_t kScratchFlagBytes = 256;
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchFlagBytes + kScratchBytes];
 
 struct dq8_ctx {
   int device;
@@ -33,6 +42,8 @@ struct dq8_ctx {
   // Device buffers that were outgrown.  A graph captured earlier may still
   // reference them, so they are freed only by dq8_destroy.
   std::vector<void*> retired;
+  // This device's address of `scratch` (null if the lookup failed).
+  uint8_t* scratch = nullptr;
 };
 
 struct dq8_weights {
@@ -57,6 +68,22 @@ struct DeviceGuard {
     if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
   }
 };
+
+// Per-device address of `scratch`, looked up once per device with that
+// device current.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch[kMaxDevices] = {};
+
+uint8_t* scratch_address(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[device]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess && p) g_scratch[device] = (uint8_t*)p;
+  }
+  return g_scratch[device];
+}
 
 dq8_status from_hip(hipError_t e) {
   if (e == hipSuccess) return DQ8_OK;
@@ -565,6 +592,7 @@ const char* dq8_status_string(dq8_status s) {
     case DQ8_ERR_FORMAT: return "invalid safetensors data";
     case DQ8_ERR_IO: return "file read failed";
     case DQ8_ERR_CAPTURE: return "the call would allocate while its stream is being captured";
+    case DQ8_ERR_LIMIT: return "the input exceeds the entry point's fixed scratch size";
   }
   return "unknown status";
 }
@@ -584,6 +612,7 @@ dq8_status dq8_create(int device, dq8_ctx** out) {
     delete ctx;
     return from_hip(e);
   }
+  ctx->scratch = scratch_address(device);  // null: dq8_apply_noalloc reports DQ8_ERR_DEVICE
   *out = ctx;
   return DQ8_OK;
 }
@@ -875,6 +904,21 @@ dq8_status dq8_apply(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t 
   return apply_paths(w->w, x, m, bias, lora, out, layout, epilogue, in, ctx->flag, s);
 }
 
+dq8_status dq8_apply_noalloc(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t m, const float* bias,
+                             const dq8_lora* lora, float* out, dq8_layout layout, dq8_epilogue epilogue,
+                             void* stream) {
+  dq8_status st = check_f32in(ctx, w, x, m, out, layout, epilogue, lora);
+  if (st != DQ8_OK || m == 0) return st;
+  if (work_q_bytes(w->w, m) + xs_pad_bytes(w->w, m) > kScratchBytes) return DQ8_ERR_LIMIT;
+  if (!ctx->scratch) return DQ8_ERR_DEVICE;
+  DeviceGuard guard(ctx->device);
+  hipStream_t s = (hipStream_t)stream;
+  uint32_t* flag = reinterpret_cast<uint32_t*>(ctx->scratch);
+  const WorkInputs in = inputs_at(w->w, m, ctx->scratch + kScratchFlagBytes);
+  st = quantize_into(w->w, x, m, in, flag, s);
+  if (st != DQ8_OK) return st;
+  return apply_paths(w->w, x, m, bias, lora, out, layout, epilogue, in, flag, s);
+}
 
 dq8_status dq8_linear_q(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, const float* scales, size_t m,
                         const float* bias, const dq8_lora* lora, float* out, dq8_epilogue epilogue, int8_t* q_out,

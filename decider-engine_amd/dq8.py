@@ -26,7 +26,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libdq8.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "dq8.h")
 
-OK, ERR_SHAPE, ERR_NONFINITE, ERR_ARG, ERR_DEVICE, ERR_NOMEM, ERR_FORMAT, ERR_IO, ERR_CAPTURE = range(9)
+OK, ERR_SHAPE, ERR_NONFINITE, ERR_ARG, ERR_DEVICE, ERR_NOMEM, ERR_FORMAT, ERR_IO, ERR_CAPTURE, ERR_LIMIT = range(10)
 F32, BF16, F16 = 0, 1, 2  # dq8_dtype
 WRITE, ADD, SWIGLU = 0, 1, 2
 ROWS, COLUMNS = 0, 1
@@ -134,6 +134,7 @@ def lib() -> ctypes.CDLL:
         "dq8_status_string": ([_i], ctypes.c_char_p),
         "dq8_linear_fp32": ([_vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
         "dq8_apply": ([_vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
+        "dq8_apply_noalloc": ([_vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
         "dq8_weights_from_raw": ([_vp, _vp, _i, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
         "dq8_weights_upload": ([_vp, _vp, _i, _sz, _sz, _vp, ctypes.POINTER(_vp)], _i),
         "dq8_st_open": ([ctypes.c_char_p, ctypes.POINTER(_vp)], _i),
@@ -526,6 +527,12 @@ class Context:
         """Projection::apply_quantized on fp32 x: the int8 path, or the FP32 path
         if x holds a non-finite value, chosen on the device."""
         return self._fp32_call("dq8_apply", w, x, out, bias, lora, layout, epilogue)
+
+    def apply_noalloc(self, w: Weights, x, out=None, bias=None, lora: Lora | None = None, layout=ROWS,
+                      epilogue=WRITE):
+        """apply() through dq8_apply_noalloc: no device allocation, inputs limited
+        by the library's fixed 16 MiB scratch (ERR_LIMIT beyond it)."""
+        return self._fp32_call("dq8_apply_noalloc", w, x, out, bias, lora, layout, epilogue)
 
     def linear_batch(self, items: list[Item]) -> None:
         torch = _torch()

@@ -63,7 +63,8 @@ typedef enum dq8_status {
     DQ8_ERR_NOMEM = 5,     /* device allocation failed */
     DQ8_ERR_FORMAT = 6,    /* a safetensors file or tensor that read_tensors / Data::read rejects */
     DQ8_ERR_IO = 7,        /* a file could not be opened or read */
-    DQ8_ERR_CAPTURE = 8    /* the stream is being captured and the call would allocate (see dq8_reserve) */
+    DQ8_ERR_CAPTURE = 8,   /* the stream is being captured and the call would allocate (see dq8_reserve) */
+    DQ8_ERR_LIMIT = 9      /* the input exceeds the fixed scratch of dq8_apply_noalloc */
 } dq8_status;
 
 /* Stored element types of weights (Data::{F32, Bf16, F16}, weights.rs:12-15),
@@ -255,6 +256,21 @@ dq8_status dq8_linear_fp32(dq8_ctx *ctx, const dq8_weights *w, const float *x, s
  * either way.  Uses the context workspace (calls of one context are ordered). */
 dq8_status dq8_apply(dq8_ctx *ctx, const dq8_weights *w, const float *x, size_t m, const float *bias,
                      const dq8_lora *lora, float *out, dq8_layout layout, dq8_epilogue epilogue, void *stream);
+/* dq8_apply that allocates nothing, ever: no counterpart in the reference.  It
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * quantized inputs, their scales and the non-finite flag live in a fixed
+ * 16 MiB device array of the library (one per GPU, held until the process
+ * ends) instead of the context workspace: ceil(m*G*64/256)*256 +
+ * ceil(m*ceil(G/4)*16/256)*256 bytes must fit in 16 MiB (G = ceil(k/64); for
+ * example 2048 x 6144 or 4096 x 2048), else DQ8_ERR_LIMIT and nothing is
+ * enqueued.  Results are those of dq8_apply, bit for bit.  All calls on one
+ * GPU share that array, whatever their context: calls that overlap on one GPU
+ * (two streams, or two host threads) race and give wrong results; each call's
+ * flag is cleared by a kernel, so stream-ordered calls need no other care. */
+dq8_status dq8_apply_noalloc(dq8_ctx *ctx, const dq8_weights *w, const float *x, size_t m, const float *bias,
+                             const dq8_lora *lora, float *out, dq8_layout layout, dq8_epilogue epilogue,
+                             void *stream);
 
 /* Several independent projections in one launch (same-shape inputs are not
  * required).  Each item is one dq8_linear (or dq8_linear_lora).  This is the shape of a model
