@@ -20,8 +20,22 @@ by layer with their rows stacked into one 384-row launch per layer set.
 
 "roofline" is for the dominant kernel (the wide projection kernel): achieved
 = algorithmic int8 ops per launch / its average launch time from HIP events on
-the launch stream.  "cpu_baseline" times the oracle (the C restatement of the
-reference's x86 path) on a bounded sample of the same workload.
+the launch stream.
+
+Further legs, each timed on its own: "config1" (one 128 x 2048 -> 2048 linear,
+seed 0), "config2" (the 512-token SwiGLU FFN block through dq8_ffn), "config3"
+(one layer's projections at 4096 tokens with 1% of the channels x20),
+"reference_benchmarks" (the reference's own timed benchmarks, tensor.rs:553-603
+and weights.rs:580-631, on their formula inputs, next to its published times)
+and "host_round_trip" (pinned host buffers in and out around the device work,
+as a caller with host-resident activations pays).
+
+"cpu_baseline" times the oracle (the C restatement of the reference's x86
+path) on a bounded sample of the stack's workload, with all usable host cores
+(at most 16) and with one, median of 5 runs.  The same leg recomputes sampled
+rows of every timed GPU workload above with the oracle and compares them bit
+for bit ("checks"); a mismatch fails the run.  With --no-cpu-baseline neither
+runs.
 """
 from __future__ import annotations
 
@@ -134,6 +148,7 @@ def main():
     gate = torch.empty((M, FFN_DIM), dtype=torch.float32, device=dev)
     resid = torch.zeros((M, HIDDEN), dtype=torch.float32, device=dev)
     flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    bufs = {"mixer": mixer_out, "k": k_out, "v": v_out, "proj": proj_out, "gate": gate, "resid": resid}
 
     def quant(x, q, s, k):
         return ("quant", lib.dq8_quantize, (ctx.handle, x.data_ptr(), M, k, q.data_ptr(), s.data_ptr(),
@@ -296,6 +311,10 @@ def main():
     achieved = lin_ops_per_launch / (lin_avg_ms * 1e-3) / 1e12
     value = step_ops / (ms_step * 1e-3) / 1e12
     lora = run_lora_stack(args, torch, stream, build, run_step, step_ops, ms_step) if rank > 0 else None
+    # outputs of the first (GDN) and last (GQA) layer of the timed step, run once more on their own from a zero
+    # residual, kept for the oracle check of the cpu_baseline leg
+    stack_checks = [capture_layer(torch, dq8, layers, calls, i, M, bufs) for i in (0, len(layers) - 1)] \
+        if not args.no_cpu_baseline else []
 
     # release the stack before the skinny workload
     for L in layers:
@@ -308,7 +327,22 @@ def main():
 
     stacked, skinny = run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen)
     load = run_load(args, torch, dq8, ctx, gen)
-    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, torch, dq8, ctx, dev, gen)
+    keep_checks = not args.no_cpu_baseline
+    config1 = run_config1(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
+    config2 = run_config2(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
+    config3 = run_config3(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
+    reference = run_reference_benchmarks(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
+    round_trip = run_host_round_trip(args, torch, dq8, ctx, lib, dev, stream)
+    cpu = None
+    if not args.no_cpu_baseline:
+        checks = {"stack_layer_0": stack_checks[0], "stack_layer_23": stack_checks[1],
+                  "config1": config1.pop("_check"), "config2": config2.pop("_check"),
+                  "config3": config3.pop("_check")}
+        for leg in reference.values():
+            for key in list(leg):
+                if key.startswith("_check"):
+                    checks[key[len("_check_"):]] = leg.pop(key)
+        cpu = run_cpu_baseline(args, torch, dq8, ctx, dev, gen, checks)
     traffic = load_traffic("linear_wide_stack2048")
     out = {
         "metric": "int8 prefill-projection TOPS (% of i8 MFMA peak); skinny-M HBM GB/s",
@@ -351,9 +385,18 @@ def main():
         "questions_stacked": stacked,
         "load": load,
         "lora": lora,
+        "config1": config1,
+        "config2": config2,
+        "config3": config3,
+        "reference_benchmarks": reference,
+        "host_round_trip": round_trip,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
+    if cpu is not None and not cpu["checks_passed"]:
+        print("bench: a sampled oracle check of the timed workloads failed: " +
+              json.dumps({k: v for k, v in cpu["checks"].items() if v != "bit-exact"}), file=sys.stderr)
+        sys.exit(1)
 
 
 def run_lora_stack(args, torch, stream, build, run_step, step_ops, base_ms):
@@ -661,49 +704,484 @@ def run_load(args, torch, dq8, ctx, gen):
     }
 
 
-def run_cpu_baseline(args, torch, dq8, ctx, dev, gen):
-    """The oracle (C restatement of the reference's x86 int8 path: per-projection
-    input quantization + per-column scalar group dots, threads over columns)
-    on the first GDN layer + its FFN for a bounded number of token rows."""
+def sample_rows(m, count, seed):
+    """count sorted distinct row indices of [0, m), always holding the first and the last row."""
+    import numpy as np
+
+    rows = np.random.default_rng(seed).choice(m, size=min(count, m), replace=False)
+    rows[0], rows[-1] = 0, m - 1
+    return np.unique(rows)
+
+
+def host_rows(torch, t, rows):
+    torch.cuda.synchronize()
+    return t[torch.as_tensor(rows, device=t.device)].cpu().numpy()
+
+
+def exported(torch, w):
+    v, s = w.export()
+    torch.cuda.synchronize()
+    return v.cpu().numpy(), s.cpu().numpy()
+
+
+def timed_calls(torch, stream, fn, reps):
+    """Device time per call of fn() over reps back-to-back calls on stream (events around the batch), in ms."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(reps):
+        fn()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / reps
+
+
+def ok(st, what):
+    if st != 0:
+        import dq8
+
+        raise dq8.Dq8Error(st, what)
+
+
+def capture_layer(torch, dq8, layers, calls, i, M, bufs):
+    """Layer i of the stack (its 9 calls of the timed step: quantize, in / q,k,v, quantize, out / o, quantize,
+    gate, up (SwiGlu), quantize h, down (Add)) run once more from a zero residual; sampled rows of its inputs,
+    outputs and weights are kept for the oracle."""
+    L = layers[i]
+    bufs["resid"].zero_()
+    for _, fn, a, _ in calls[9 * i: 9 * i + 9]:
+        ok(fn(*a), fn.__name__)
+    torch.cuda.synchronize()
+    rows = sample_rows(M, 16, 100 + i)
+    x, mix, ffn = (host_rows(torch, L[key], rows) for key in ("x", "mix", "ffn"))
+    items = []
+    if L["kind"] == "gdn":
+        items.append(("linear", x, *exported(torch, L["in"]), None, 0, host_rows(torch, bufs["mixer"], rows)))
+        items.append(("linear", mix, *exported(torch, L["out"]), None, 0, host_rows(torch, bufs["proj"], rows)))
+    else:
+        q_view = bufs["mixer"].view(-1)[:M * HIDDEN].view(M, HIDDEN)
+        for name, buf in (("q", q_view), ("k", bufs["k"]), ("v", bufs["v"])):
+            items.append(("linear", x, *exported(torch, L[name]), None, 0, host_rows(torch, buf, rows)))
+        items.append(("linear", mix, *exported(torch, L["o"]), None, 0, host_rows(torch, bufs["proj"], rows)))
+    h = host_rows(torch, bufs["gate"], rows)
+    items.append(("ffn_h", ffn, exported(torch, L["gate"]), exported(torch, L["up"]), h))
+    items.append(("linear", h, *exported(torch, L["down"]), np_zeros(len(rows), HIDDEN), 1,
+                  host_rows(torch, bufs["resid"], rows)))
+    return {"what": f"layer {i} ({L['kind']}) of the timed step, {len(rows)} sampled rows", "items": items}
+
+
+def np_zeros(*shape):
+    import numpy as np
+
+    return np.zeros(shape, np.float32)
+
+
+def run_config1(args, torch, dq8, ctx, lib, dev, stream, keep):
+    """Single linear M=128, K=N=2048, weights N(0, 0.02^2), activations N(0, 1), seed 0: quantize + project."""
+    import numpy as np
+
+    M, K, N = 128, HIDDEN, HIDDEN
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    h = ctx.weights_from_f32(torch.from_numpy(w).to(dev))
+    xd = torch.from_numpy(x).to(dev)
+    q = torch.empty((M, K), dtype=torch.int8, device=dev)
+    s = torch.empty((M, K // 64), dtype=torch.float32, device=dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    sh = stream.cuda_stream
+    quant = lambda: ok(lib.dq8_quantize(ctx.handle, xd.data_ptr(), M, K, q.data_ptr(), s.data_ptr(), flag.data_ptr(),
+                                        sh), "dq8_quantize")
+    lin = lambda: ok(lib.dq8_linear(ctx.handle, h.handle, q.data_ptr(), s.data_ptr(), M, None, out.data_ptr(),
+                                    dq8.ROWS, dq8.WRITE, sh), "dq8_linear")
+    ms = timed_calls(torch, stream, lambda: (quant(), lin()), 50)
+    ms_lin = timed_calls(torch, stream, lin, 50)
+    ops = 2 * M * N * K
+    gemm_bytes = N * K + 4 * N * (K // 64) + M * K + 4 * M * (K // 64) + 4 * M * N
+    res = {
+        "workload": "single int8 linear, 128 tokens x 2048 -> 2048, seed 0 (weights N(0,0.02^2), x N(0,1)); "
+                    "quantize + project, back-to-back calls",
+        "ms": round(ms, 5), "tops": round(ops / (ms * 1e-3) / 1e12, 2),
+        "projection_ms": round(ms_lin, 5), "projection_tops": round(ops / (ms_lin * 1e-3) / 1e12, 2),
+        "projection_gbs": round(gemm_bytes / (ms_lin * 1e-3) / 1e9, 1),
+    }
+    res["_check"] = {"what": "all 128 rows", "items": [("linear_w", x, w, None, 0, host_rows(torch, out, np.arange(M)))]} \
+        if keep else None
+    h.free()
+    return res
+
+
+def run_config2(args, torch, dq8, ctx, lib, dev, stream, keep):
+    """SwiGLU FFN block for a 512-token prompt (dq8_ffn: gate Write, up SwiGlu, h re-quantized, down Add)."""
+    import numpy as np
+
+    M = 512
+    rng = np.random.default_rng(2)
+    ws = {nm: (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+          for nm, n, k in (("gate", FFN_DIM, HIDDEN), ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM))}
+    x = rng.standard_normal((M, HIDDEN)).astype(np.float32)
+    W = {nm: ctx.weights_from_f32(torch.from_numpy(w).to(dev)) for nm, w in ws.items()}
+    xd = torch.from_numpy(x).to(dev)
+    q = torch.empty((M, HIDDEN), dtype=torch.int8, device=dev)
+    s = torch.empty((M, HIDDEN // 64), dtype=torch.float32, device=dev)
+    hbuf = torch.empty((M, FFN_DIM), dtype=torch.float32, device=dev)
+    resid = torch.zeros((M, HIDDEN), dtype=torch.float32, device=dev)
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step():
+        ok(lib.dq8_quantize(ctx.handle, xd.data_ptr(), M, HIDDEN, q.data_ptr(), s.data_ptr(), flag.data_ptr(),
+                            stream.cuda_stream), "dq8_quantize")
+        ctx.ffn(W["gate"], W["up"], W["down"], q, s, resid, h=hbuf, nonfinite=flag)
+
+    ms = timed_calls(torch, stream, step, 30)
+    ops = 2 * M * (2 * FFN_DIM * HIDDEN + HIDDEN * FFN_DIM)
+    res = {
+        "workload": "SwiGLU FFN block, 512 tokens: gate/up 2048->6144, silu(gate)*up, re-quantized, down 6144->2048 "
+                    "Add; seed 2; input quantization included (dq8_quantize + dq8_ffn)",
+        "ms": round(ms, 5), "tops": round(ops / (ms * 1e-3) / 1e12, 2),
+        "weight_gbs": round(3 * FFN_DIM * HIDDEN * (1 + 4 / 64) / (ms * 1e-3) / 1e9, 1),
+    }
+    check = None
+    if keep:
+        resid.zero_()
+        step()
+        rows = sample_rows(M, 32, 2)
+        h = host_rows(torch, hbuf, rows)
+        check = {"what": f"{len(rows)} sampled rows of h and the residual", "items": [
+            ("ffn_h_w", x[rows], ws["gate"], ws["up"], h),
+            ("linear_w", h, ws["down"], np_zeros(len(rows), HIDDEN), 1, host_rows(torch, resid, rows))]}
+    res["_check"] = check
+    for w in W.values():
+        w.free()
+    return res
+
+
+def run_config3(args, torch, dq8, ctx, lib, dev, stream, keep):
+    """One layer's projection set at the 4096-token window with 1% of the channels x20: GQA q/k/v (one grouped
+    launch) and o, Gated DeltaNet in (q,k,v,z + b,a) and out, each input quantized."""
+    import numpy as np
+
+    M = 4096
+    rng = np.random.default_rng(3)
+
+    def outliers():
+        a = rng.standard_normal((M, HIDDEN)).astype(np.float32)
+        a[:, rng.choice(HIDDEN, size=HIDDEN // 100, replace=False)] *= np.float32(20.0)
+        return a
+
+    shapes = [("q", HIDDEN), ("k", 512), ("v", 512), ("o", HIDDEN), ("gdn_in", GDN_IN), ("gdn_out", HIDDEN)]
+    ws = {nm: (rng.standard_normal((n, HIDDEN)) * 0.02).astype(np.float32) for nm, n in shapes}
+    xs = {"x": outliers(), "attn": outliers(), "rec": outliers()}
+    src = {"q": "x", "k": "x", "v": "x", "gdn_in": "x", "o": "attn", "gdn_out": "rec"}
+    W = {nm: ctx.weights_from_f32(torch.from_numpy(w).to(dev)) for nm, w in ws.items()}
+    X = {k: torch.from_numpy(v).to(dev) for k, v in xs.items()}
+    Q = {k: (torch.empty((M, HIDDEN), dtype=torch.int8, device=dev),
+             torch.empty((M, HIDDEN // 64), dtype=torch.float32, device=dev)) for k in xs}
+    out = {nm: torch.empty((M, n), dtype=torch.float32, device=dev) for nm, n in shapes}
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    sh = stream.cuda_stream
+    qkv = (dq8._Item * 3)()
+    for i, nm in enumerate(("q", "k", "v")):
+        qkv[i] = dq8._Item(W[nm].handle, Q["x"][0].data_ptr(), Q["x"][1].data_ptr(), M, None, out[nm].data_ptr(),
+                           dq8.ROWS, dq8.WRITE)
+
+    def step():
+        for k in xs:
+            ok(lib.dq8_quantize(ctx.handle, X[k].data_ptr(), M, HIDDEN, Q[k][0].data_ptr(), Q[k][1].data_ptr(),
+                                flag.data_ptr(), sh), "dq8_quantize")
+            if k == "x":
+                ok(lib.dq8_linear_batch(ctx.handle, qkv, 3, sh), "dq8_linear_batch")
+                nms = ("gdn_in",)
+            else:
+                nms = ("o",) if k == "attn" else ("gdn_out",)
+            for nm in nms:
+                ok(lib.dq8_linear(ctx.handle, W[nm].handle, Q[k][0].data_ptr(), Q[k][1].data_ptr(), M, None,
+                                  out[nm].data_ptr(), dq8.ROWS, dq8.WRITE, sh), "dq8_linear")
+
+    ms = timed_calls(torch, stream, step, 20)
+    ops = sum(2 * M * n * HIDDEN for _, n in shapes)
+    res = {
+        "workload": "one layer's projections at the 4096-token window: GQA q 2048->2048, k/v 2048->512 (grouped), "
+                    "o 2048->2048; Gated DeltaNet in 2048->8224, out 2048->2048; inputs N(0,1) with 1% of the "
+                    "channels x20; seed 3; the 3 input quantizations included",
+        "ms": round(ms, 5), "tops": round(ops / (ms * 1e-3) / 1e12, 2),
+        "frac_of_int8_peak": round(ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+    }
+    check = None
+    if keep:
+        torch.cuda.synchronize()
+        rows = sample_rows(M, 16, 3)
+        check = {"what": f"{len(rows)} sampled rows of each projection", "items": [
+            ("linear_w", xs[src[nm]][rows], ws[nm], None, 0, host_rows(torch, out[nm], rows)) for nm, _ in shapes]}
+    res["_check"] = check
+    for w in W.values():
+        w.free()
+    return res
+
+
+def run_reference_benchmarks(args, torch, dq8, ctx, lib, dev, stream, keep):
+    """The reference's own timed benchmarks on their formula inputs, through dq8_apply (quantization included,
+    as in their timed region), next to the numbers the reference publishes for them (ARM64 CI runner, NEON SDOT,
+    4 workers, mean of 3; docs/lambda.md)."""
+    import numpy as np
+
+    sh = stream.cuda_stream
+    res = {}
+    # tensor.rs:553-603 benchmark_int8_projections: 2048x2048, values ((i*71 % 255) - 127) as u8, scales 1/127,
+    # x = ((i*43 % 255) - 127)/127, rows 1 / 32 / 128, int8 compute
+    K = N = 2048
+    values = ((np.arange(N * K, dtype=np.int64) * 71 % 255).astype(np.int16) - 127).astype(np.uint8).reshape(N, K)
+    scales = np.full((N, K // 64), np.float32(1.0) / np.float32(127.0), np.float32)
+    h = ctx.weights_from_quantized(torch.from_numpy(values).to(dev), torch.from_numpy(scales).to(dev))
+    published = {1: 0.097, 32: 1.866, 128: 7.220}
+    leg = {"workload": "tensor.rs:553-603 benchmark_int8_projections: 2048x2048 int8 compute, formula inputs, "
+                       "quantization included (dq8_apply), back-to-back calls", "rows": {}}
+    for rows in (1, 32, 128):
+        x = ((np.arange(rows * K, dtype=np.int64) * 43 % 255).astype(np.float32) - np.float32(127.0)) / \
+            np.float32(127.0)
+        xd = torch.from_numpy(x.reshape(rows, K)).to(dev)
+        out = torch.empty((rows, N), dtype=torch.float32, device=dev)
+        ms = timed_calls(torch, stream, lambda: ok(lib.dq8_apply(ctx.handle, h.handle, xd.data_ptr(), rows, None, None,
+                                                                 out.data_ptr(), dq8.ROWS, dq8.WRITE, sh),
+                                                   "dq8_apply"), 50)
+        leg["rows"][str(rows)] = {"ms": round(ms, 5), "gops": round(2 * rows * N * K / (ms * 1e-3) / 1e9, 1),
+                                  "published_arm_ms": published[rows],
+                                  "speedup_vs_published": round(published[rows] / ms, 1)}
+        if keep:
+            leg[f"_check_int8_projections_rows{rows}"] = {"what": f"{rows} rows, all outputs", "items": [
+                ("linear", x.reshape(rows, K), values, scales, None, 0, host_rows(torch, out, np.arange(rows)))]}
+    h.free()
+    res["int8_projections"] = leg
+    # weights.rs:580-631 benchmark_fused_projection: 2048 -> 6144 int8 compute + rank-16 LoRA (scale 0.5) +
+    # SwiGlu store into gate, BF16-valued matrices ((i*17 % 89) - 44)/64, x = ((i*43 % 113) - 56)/127,
+    # gate = ((i*53 % 127) - 63)/32, rows 32 / 128, fused
+    K, N, R = HIDDEN, FFN_DIM, 16
+    packed = lambda n: ((np.arange(n, dtype=np.int64) * 17 % 89).astype(np.float32) - np.float32(44.0)) / \
+        np.float32(64.0)
+    w = packed(N * K).reshape(N, K)
+    a = packed(R * K).reshape(R, K)
+    b = packed(N * R).reshape(N, R)
+    h = ctx.weights_from_f32(torch.from_numpy(w).to(dev))
+    ad, bd = torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev)
+    published = {32: 7.573, 128: 29.630}
+    leg = {"workload": "weights.rs:580-631 benchmark_fused_projection: 2048->6144 int8 compute + rank-16 LoRA "
+                       "(scale 0.5) + SwiGlu store, formula inputs; per call: gate restored, middle product "
+                       "(dq8_lora_mid), projection with adapter and fused SwiGlu (dq8_apply); back-to-back calls",
+           "rows": {}}
+    for rows in (32, 128):
+        x = ((np.arange(rows * K, dtype=np.int64) * 43 % 113).astype(np.float32) - np.float32(56.0)) / \
+            np.float32(127.0)
+        g0 = ((np.arange(rows * N, dtype=np.int64) * 53 % 127).astype(np.float32) - np.float32(63.0)) / \
+            np.float32(32.0)
+        xd = torch.from_numpy(x.reshape(rows, K)).to(dev)
+        gd0 = torch.from_numpy(g0.reshape(rows, N)).to(dev)
+        gate = gd0.clone()
+        mid = torch.empty((rows, R), dtype=torch.float32, device=dev)
+        lo = dq8._Lora(mid.data_ptr(), bd.data_ptr(), R, 0.5)
+
+        def call():
+            gate.copy_(gd0)
+            ok(lib.dq8_lora_mid(ctx.handle, xd.data_ptr(), rows, K, ad.data_ptr(), R, mid.data_ptr(), sh),
+               "dq8_lora_mid")
+            ok(lib.dq8_apply(ctx.handle, h.handle, xd.data_ptr(), rows, None, ctypes.byref(lo), gate.data_ptr(),
+                             dq8.ROWS, dq8.SWIGLU, sh), "dq8_apply")
+
+        ms = timed_calls(torch, stream, call, 50)
+        leg["rows"][str(rows)] = {"ms": round(ms, 5), "base_gops": round(2 * rows * N * K / (ms * 1e-3) / 1e9, 1),
+                                  "published_arm_ms": published[rows],
+                                  "speedup_vs_published": round(published[rows] / ms, 1)}
+        if keep:
+            call()
+            leg[f"_check_fused_projection_rows{rows}"] = {"what": f"{rows} rows, all outputs", "items": [
+                ("linear_lora_w", x.reshape(rows, K), w, a, b, 0.5, g0.reshape(rows, N), 2,
+                 host_rows(torch, gate, np.arange(rows)))]}
+    h.free()
+    res["fused_projection"] = leg
+    return res
+
+
+def run_host_round_trip(args, torch, dq8, ctx, lib, dev, stream):
+    """What a caller whose activations live in host memory pays (the crate's projections take host slices,
+    tensor.rs:379-383): pinned host input -> device, the projection, result -> pinned host, synchronized; wall
+    time per call on the host, against the device-only time of the same work.  Shapes of the multi-question
+    continuation: 24 tokens."""
+    import numpy as np
+
+    M = args.question_tokens
+    sh = stream.cuda_stream
+    res = {"workload": f"{M} tokens: one 2048->2048 projection (dq8_apply), and one question's layer set (3 inputs "
+                       f"quantized, one grouped launch of the 9 projections); pinned H2D, device work, pinned D2H, "
+                       f"stream synchronize; host wall time, median of 50"}
+    w = ctx.weights_from_f32((torch.randn((HIDDEN, HIDDEN), device=dev) * 0.02).contiguous())
+    xh = torch.randn((M, HIDDEN)).pin_memory()
+    oh = torch.empty((M, HIDDEN)).pin_memory()
+    xd = torch.empty((M, HIDDEN), device=dev)
+    od = torch.empty((M, HIDDEN), device=dev)
+    proj = lambda: ok(lib.dq8_apply(ctx.handle, w.handle, xd.data_ptr(), M, None, None, od.data_ptr(), dq8.ROWS,
+                                    dq8.WRITE, sh), "dq8_apply")
+
+    def wall(fn, reps=50):
+        for _ in range(5):
+            fn()
+        ts = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return sorted(ts)[reps // 2] * 1e3
+
+    def trip():
+        xd.copy_(xh, non_blocking=True)
+        proj()
+        oh.copy_(od, non_blocking=True)
+        stream.synchronize()
+
+    def dev_only():
+        proj()
+        stream.synchronize()
+
+    res["projection"] = {"round_trip_ms": round(wall(trip), 4), "device_sync_ms": round(wall(dev_only), 4),
+                         "device_ms": round(timed_calls(torch, stream, proj, 50), 5),
+                         "h2d_bytes": M * HIDDEN * 4, "d2h_bytes": M * HIDDEN * 4}
+    w.free()
+    shapes = [("q", HIDDEN, HIDDEN), ("k", 512, HIDDEN), ("v", 512, HIDDEN), ("o", HIDDEN, HIDDEN),
+              ("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN), ("gate", FFN_DIM, HIDDEN),
+              ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
+    src = {"q": 0, "k": 0, "v": 0, "gdn_in": 0, "gate": 0, "up": 0, "o": 1, "gdn_out": 1, "down": 2}
+    widths = [HIDDEN, HIDDEN, FFN_DIM]
+    W = [ctx.weights_from_f32((torch.randn((n, k), device=dev) * 0.02).contiguous()) for _, n, k in shapes]
+    ins_h = [torch.randn((M, k)).pin_memory() for k in widths]
+    ins_d = [torch.empty((M, k), device=dev) for k in widths]
+    qs = [(torch.empty((M, k), dtype=torch.int8, device=dev),
+           torch.empty((M, (k + 63) // 64), dtype=torch.float32, device=dev)) for k in widths]
+    outs_d = [torch.empty((M, n), device=dev) for _, n, _ in shapes]
+    outs_h = [torch.empty((M, n)).pin_memory() for _, n, _ in shapes]
+    flag = torch.zeros(1, dtype=torch.int32, device=dev)
+    items = (dq8._Item * len(shapes))()
+    for j, (nm, n, k) in enumerate(shapes):
+        q, s = qs[src[nm]]
+        items[j] = dq8._Item(W[j].handle, q.data_ptr(), s.data_ptr(), M, None, outs_d[j].data_ptr(), dq8.ROWS,
+                             dq8.WRITE)
+
+    def layer_dev():
+        for i, k in enumerate(widths):
+            ok(lib.dq8_quantize(ctx.handle, ins_d[i].data_ptr(), M, k, qs[i][0].data_ptr(), qs[i][1].data_ptr(),
+                                flag.data_ptr(), sh), "dq8_quantize")
+        ok(lib.dq8_linear_batch(ctx.handle, items, len(shapes), sh), "dq8_linear_batch")
+
+    def layer_trip():
+        for i in range(len(widths)):
+            ins_d[i].copy_(ins_h[i], non_blocking=True)
+        layer_dev()
+        for o_h, o_d in zip(outs_h, outs_d):
+            o_h.copy_(o_d, non_blocking=True)
+        stream.synchronize()
+
+    def layer_sync():
+        layer_dev()
+        stream.synchronize()
+
+    res["question_layer_set"] = {
+        "round_trip_ms": round(wall(layer_trip, 30), 4), "device_sync_ms": round(wall(layer_sync, 30), 4),
+        "device_ms": round(timed_calls(torch, stream, layer_dev, 30), 5),
+        "h2d_bytes": sum(M * k * 4 for k in widths), "d2h_bytes": sum(M * n * 4 for _, n, _ in shapes)}
+    for x in W:
+        x.free()
+    return res
+
+
+def run_checks(dq8o, checks, threads):
+    """Each check item recomputed by the oracle on the host and compared bit for bit with the GPU's bits."""
+    import numpy as np
+
+    def same(a, b):
+        a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+        return a.shape == b.shape and a.tobytes() == b.tobytes()
+
+    out = {}
+    for name, chk in checks.items():
+        if chk is None:
+            continue
+        bad = []
+        for j, it in enumerate(chk["items"]):
+            kind = it[0]
+            if kind in ("linear", "linear_w"):
+                if kind == "linear":
+                    _, x, wv, ws, result, ep, got = it
+                else:
+                    _, x, wf, result, ep, got = it
+                    wv, ws = dq8o.quantize_weights(wf)
+                want = dq8o.linear(x, wv, ws, result=result, epilogue=ep, threads=threads)
+            elif kind in ("ffn_h", "ffn_h_w"):
+                _, x, g, u, got = it
+                if kind == "ffn_h_w":
+                    g, u = dq8o.quantize_weights(g), dq8o.quantize_weights(u)
+                gate = dq8o.linear(x, *g, threads=threads)
+                want = dq8o.linear(x, *u, result=gate, epilogue=2, threads=threads)
+            elif kind == "linear_lora_w":
+                _, x, wf, a, b, scale, result, ep, got = it
+                wv, ws = dq8o.quantize_weights(wf)
+                want = dq8o.linear_lora(x, wv, ws, a, b, scale, result=result, epilogue=ep, threads=threads)
+            else:
+                raise ValueError(kind)
+            if not same(got, want):
+                bad.append(j)
+        out[name] = "bit-exact" if not bad else f"MISMATCH in items {bad} ({chk['what']})"
+    return out
+
+
+def run_cpu_baseline(args, torch, dq8, ctx, dev, gen, checks):
+    """The oracle (C restatement of the reference's x86 int8 path: per-projection input quantization +
+    per-column scalar group dots, threads over output columns as rayon does, tensor.rs:442-448) on a sample of
+    the stack's workload: one GDN layer's projections + its FFN for a bounded number of token rows.  One
+    warm-up, then the median of 5 timed runs, with all usable host cores and with one.  Then the sampled oracle
+    checks of the timed GPU workloads."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
     import dq8o
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nproc = os.cpu_count() or 1
+    # at most 16 threads: one GPU's share of the host
+    threads = max(1, min(16, nproc, int(os.environ.get("OMP_NUM_THREADS", "16") or 16)))
     rng = np.random.default_rng(5)
     shapes = [("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN), ("gate", FFN_DIM, HIDDEN),
               ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
     ws = {}
     for name, n, k in shapes:
         h = ctx.weights_from_f32((torch.randn((n, k), generator=gen, device=dev) * 0.02).contiguous())
-        v, s = h.export()
-        torch.cuda.synchronize()
-        ws[name] = (v.cpu().numpy(), s.cpu().numpy())
+        ws[name] = exported(torch, h)
         h.free()
 
-    def layer(rows):
-        x = rng.standard_normal((rows, HIDDEN)).astype(np.float32)
-        t = time.perf_counter()
-        dq8o.linear(x, *ws["gdn_in"], threads=threads)
-        dq8o.linear(x, *ws["gdn_out"], threads=threads)
-        g = dq8o.linear(x, *ws["gate"], threads=threads)
-        g = dq8o.linear(x, *ws["up"], result=g, epilogue=2, threads=threads)
-        dq8o.linear(g, *ws["down"], result=x, epilogue=1, threads=threads)
-        return time.perf_counter() - t
+    def layer(x, t):
+        s = time.perf_counter()
+        dq8o.linear(x, *ws["gdn_in"], threads=t)
+        dq8o.linear(x, *ws["gdn_out"], threads=t)
+        g = dq8o.linear(x, *ws["gate"], threads=t)
+        g = dq8o.linear(x, *ws["up"], result=g, epilogue=2, threads=t)
+        dq8o.linear(g, *ws["down"], result=x, epilogue=1, threads=t)
+        return time.perf_counter() - s
 
     ops_per_row = 2 * sum(n * k for _, n, k in shapes)
-    rows = 16
-    secs = layer(rows)
-    # size the sample to about cpu_seconds of work (per-row cost measured on the previous sample)
-    while secs < 0.5 * args.cpu_seconds and rows < 2048:
-        rows = int(max(rows + 1, min(2048, rows * args.cpu_seconds / max(secs, 1e-6))))
-        secs = layer(rows)
-    # a whole 2048-token layer shorter than the target: time that many layers back to back
-    n_layers = 1
-    if secs < 0.5 * args.cpu_seconds:
-        n_layers = max(1, int(round(args.cpu_seconds / secs)))
-        secs = sum(layer(rows) for _ in range(n_layers))
+    # size the sample so that one single-thread run takes about cpu_seconds / 10
+    probe = rng.standard_normal((4, HIDDEN)).astype(np.float32)
+    per_row = layer(probe, 1) / 4
+    rows = int(max(8, min(512, args.cpu_seconds / 10 / per_row)))
+    x = rng.standard_normal((rows, HIDDEN)).astype(np.float32)
+
+    def median_tops(t):
+        layer(x, t)
+        secs = sorted(layer(x, t) for _ in range(5))[2]
+        return ops_per_row * rows / secs / 1e12, secs
+
+    tops, secs = median_tops(threads)
+    tops1, secs1 = median_tops(1)
     cpu_model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -713,13 +1191,20 @@ def run_cpu_baseline(args, torch, dq8, ctx, dev, gen):
                     break
     except OSError:
         pass
+    results = run_checks(dq8o, checks, threads)
     return {
-        "value": round(ops_per_row * rows * n_layers / secs / 1e12, 5),
+        "value": round(tops, 5),
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n_layers} x (GDN layer + FFN projections: in 2048->8224, out, gate/up SwiGlu, re-quantized "
-                  f"down) for {rows} of the 2048 tokens, quantization included; {secs:.1f} s on {cpu_model}",
+        "sample": f"GDN layer + FFN projections (in 2048->8224, out, gate/up SwiGlu, re-quantized down) for {rows} "
+                  f"of the stack's 2048 tokens, quantization included; median of 5 runs after 1 warm-up "
+                  f"({secs:.2f} s each at {threads} threads, {secs1:.2f} s at 1) on {cpu_model}",
+        "value_1_thread": round(tops1, 5),
+        "nproc": nproc,
+        "cpu_model": cpu_model,
+        "checks": results,
+        "checks_passed": all(v == "bit-exact" for v in results.values()),
     }
 
 
