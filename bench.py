@@ -197,8 +197,11 @@ def main():
                                                   ctypes.byref(lo), out.data_ptr(), dq8.ROWS, ep, sh),
                  (0, 2 * M * w.n * w.k))]
 
+    layer_bounds = []  # [start, end) of each layer's calls in the last build
+
     def build(with_lora):
         calls = []
+        layer_bounds.clear()
 
         def proj(L, name, x, q, s, out, ep, mid, k, with_mid=True):
             if with_lora:
@@ -207,6 +210,7 @@ def main():
                 calls.append(linear(L[name], q, s, out, ep))
 
         for L in layers:
+            layer_bounds.append(len(calls))
             calls.append(quant(L["x"], qx, sx, HIDDEN))
             if L["kind"] == "gdn":
                 proj(L, "in", L["x"], qx, sx, mixer_out, dq8.WRITE, mids["a"], HIDDEN)
@@ -237,13 +241,23 @@ def main():
             if with_lora:  # gate and up share their input: one grouped launch of their middle products
                 calls.append(mid_batch_call([(L["ffn"], lora_of(L, "gate")[0], mids["b"], HIDDEN),
                                              (L["ffn"], lora_of(L, "up")[0], mids["c"], HIDDEN)]))
-            proj(L, "gate", L["ffn"], qx, sx, gate, dq8.WRITE, mids["b"], HIDDEN, with_mid=False)
-            proj(L, "up", L["ffn"], qx, sx, gate, dq8.SWIGLU, mids["c"], HIDDEN, with_mid=False)
-            calls.append(quant(gate, qf, sf, FFN_DIM))
-            proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
+                proj(L, "gate", L["ffn"], qx, sx, gate, dq8.WRITE, mids["b"], HIDDEN, with_mid=False)
+                proj(L, "up", L["ffn"], qx, sx, gate, dq8.SWIGLU, mids["c"], HIDDEN, with_mid=False)
+                calls.append(quant(gate, qf, sf, FFN_DIM))
+                proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
+            else:
+                # gate and up in one launch storing h (qwen.rs:489-490), h re-quantized, down Add
+                ops = sum(2 * M * L[n].n * L[n].k for n in ("gate", "up"))
+                calls.append(("linear", lib.dq8_ffn_gate_up, (ctx.handle, L["gate"].handle, L["up"].handle,
+                                                              qx.data_ptr(), sx.data_ptr(), M, None, None,
+                                                              gate.data_ptr(), sh), (0, ops)))
+                calls.append(quant(gate, qf, sf, FFN_DIM))
+                proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
+        layer_bounds.append(len(calls))
         return calls
 
     calls = build(False)
+    bounds = list(layer_bounds)
     step_ops = sum(c[3][1] for c in calls)
 
     def run_step(events=None, calls=calls):
@@ -313,7 +327,8 @@ def main():
     lora = run_lora_stack(args, torch, stream, build, run_step, step_ops, ms_step) if rank > 0 else None
     # outputs of the first (GDN) and last (GQA) layer of the timed step, run once more on their own from a zero
     # residual, kept for the oracle check of the cpu_baseline leg
-    stack_checks = [capture_layer(torch, dq8, layers, calls, i, M, bufs) for i in (0, len(layers) - 1)] \
+    stack_checks = [capture_layer(torch, dq8, layers, calls[bounds[i]:bounds[i + 1]], i, M, bufs)
+                    for i in (0, len(layers) - 1)] \
         if not args.no_cpu_baseline else []
 
     # release the stack before the skinny workload
@@ -746,12 +761,12 @@ def ok(st, what):
 
 
 def capture_layer(torch, dq8, layers, calls, i, M, bufs):
-    """Layer i of the stack (its 9 calls of the timed step: quantize, in / q,k,v, quantize, out / o, quantize,
-    gate, up (SwiGlu), quantize h, down (Add)) run once more from a zero residual; sampled rows of its inputs,
-    outputs and weights are kept for the oracle."""
+    """Layer i of the stack (its calls of the timed step: quantize, in / q,k,v, quantize, out / o, quantize,
+    the FFN chain: gate and up (SwiGlu) storing h, h re-quantized, down (Add)) run once more from a zero
+    residual; sampled rows of its inputs, outputs and weights are kept for the oracle."""
     L = layers[i]
     bufs["resid"].zero_()
-    for _, fn, a, _ in calls[9 * i: 9 * i + 9]:
+    for _, fn, a, _ in calls:
         ok(fn(*a), fn.__name__)
     torch.cuda.synchronize()
     rows = sample_rows(M, 16, 100 + i)

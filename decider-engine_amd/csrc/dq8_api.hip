@@ -173,6 +173,10 @@ void fill_proj(dq8::Proj& p, const dq8::Weights& w, const int8_t* q, int ldq, co
   p.np = w.np;
   p.epilogue = epilogue;
   p.layout = layout;
+  p.wt2 = nullptr;
+  p.wst2 = nullptr;
+  p.bias2 = nullptr;
+  p.pair = 0;
 }
 
 // Wide kernel: split the tile grid into gm x gn regions, gm * gn = 8, one per
@@ -214,9 +218,11 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips) {
   p.xcd_gm = 0;
   p.nseg = 1;
   if (kind == 0) {
-    p.waves_n = p.np / dq8::wide_block_cols();
+    // a SwiGLU pair's block covers half as many outputs of each projection
+    p.waves_n = p.pair ? (p.n + dq8::wide_block_cols() / 2 - 1) / (dq8::wide_block_cols() / 2)
+                       : p.np / dq8::wide_block_cols();
     const int row_tiles = (p.m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows();
-    p.xcd_gm = xcd_rows_split(row_tiles, p.waves_n, (size_t)p.m * p.g, (size_t)p.n * p.g);
+    p.xcd_gm = xcd_rows_split(row_tiles, p.waves_n, (size_t)p.m * p.g, (size_t)(p.pair ? 2 : 1) * p.n * p.g);
     b.total_waves += p.waves_n * row_tiles;
   } else {
     p.nseg = dq8::skinny_segments(p.g, few_strips);
@@ -369,6 +375,37 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     const dq8::Weights& w = items[0].w->w;
     hipError_t e = dq8::launch_quantize(items[0].out, (int)items[0].m, w.n, qout->q, w.n, qout->scales,
                                         (w.n + kGroup - 1) / kGroup, qout->nonfinite, s);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  return DQ8_OK;
+}
+
+// One layer's gate and up projections (same shape, shared quantized input,
+// no adapters) in one wide launch that stores h = silu(gate + bias) * (up +
+// bias2) into h [m][n], then quantizes h as qout asks.  The results equal the
+// separate Write and SwiGlu launches bit for bit: each output's arithmetic is
+// unchanged, only the two tiles of one output sit in one wave.
+dq8_status run_pair(dq8_ctx* ctx, const dq8::Weights& g, const dq8::Weights& u, const int8_t* q, const float* xs,
+                    size_t m, const float* gate_bias, const float* up_bias, float* h, const QOut* qout,
+                    hipStream_t s) {
+  (void)ctx;
+  dq8::Batch b;
+  b.count = 1;
+  b.total_waves = 0;
+  b.any_lora = 0;
+  b.unless = nullptr;
+  dq8::Proj& p = b.p[0];
+  fill_proj(p, g, q, g.k, xs, g.g, m, gate_bias, h, nullptr, DQ8_ROWS, DQ8_WRITE, nullptr);
+  p.wt2 = u.values;
+  p.wst2 = u.scales;
+  p.bias2 = up_bias;
+  p.pair = 1;
+  place_proj(p, 0, b, false);
+  hipError_t e = dq8::launch_linear(b, 0, false, s);
+  if (e != hipSuccess) return from_hip(e);
+  if (qout) {
+    e = dq8::launch_quantize(h, (int)m, g.n, qout->q, g.n, qout->scales, (g.n + kGroup - 1) / kGroup,
+                             qout->nonfinite, s);
     if (e != hipSuccess) return from_hip(e);
   }
   return DQ8_OK;
@@ -799,6 +836,26 @@ dq8_status check_mid(const float* x, size_t m, size_t k, const float* a, size_t 
     return DQ8_ERR_SHAPE;  // the last bound keeps the grid under 2^32 work-items
   return DQ8_OK;
 }
+// Whether the gate and up projections of an FFN can run as one SwiGLU pair
+// launch: the wide kernel (more than 64 rows), no adapters, inputs the kernel
+// reads as they are.
+bool pair_ok(const dq8::Weights& g, const int8_t* q, const float* xs, size_t m) {
+  return kind_of(g, m) == 0 && m > 64 && !needs_pad(g, q) && !needs_xs_pad(g, xs);
+}
+
+// gate Write into h, then up SwiGlu into h; one launch when pair_ok.
+dq8_status gate_up(dq8_ctx* ctx, const dq8_weights* gate, const dq8_weights* up, const int8_t* q, const float* xs,
+                   size_t m, const float* gate_bias, const float* up_bias, const dq8_lora* gate_lora,
+                   const dq8_lora* up_lora, float* h, const QOut* qout, hipStream_t s) {
+  if (!gate_lora && !up_lora && pair_ok(gate->w, q, xs, m))
+    return run_pair(ctx, gate->w, up->w, q, xs, m, gate_bias, up_bias, h, qout, s);
+  dq8_linear_item gi = {gate, q, xs, m, gate_bias, h, DQ8_ROWS, DQ8_WRITE, gate_lora};
+  dq8_status st = run_linear(ctx, &gi, 1, nullptr, s);
+  if (st != DQ8_OK) return st;
+  dq8_linear_item ui = {up, q, xs, m, up_bias, h, DQ8_ROWS, DQ8_SWIGLU, up_lora};
+  return run_linear(ctx, &ui, 1, nullptr, s, qout);
+}
+
 }  // namespace
 
 extern "C" {
@@ -867,6 +924,19 @@ dq8_status dq8_linear_batch(dq8_ctx* ctx, const dq8_linear_item* items, size_t c
   }
   DeviceGuard guard(ctx->device);
   return run_linear(ctx, items, count, nullptr, (hipStream_t)stream);
+}
+
+dq8_status dq8_ffn_gate_up(dq8_ctx* ctx, const dq8_weights* gate, const dq8_weights* up, const int8_t* q,
+                           const float* scales, size_t m, const float* gate_bias, const float* up_bias, float* h,
+                           void* stream) {
+  if (!ctx || !gate || !up) return DQ8_ERR_ARG;
+  if (m == 0) return DQ8_OK;
+  if (gate->w.k != up->w.k || gate->w.n != up->w.n) return DQ8_ERR_SHAPE;
+  dq8_status st = check_item_args(gate, q, scales, m, h, DQ8_ROWS, DQ8_WRITE);
+  if (st != DQ8_OK) return st;
+  if (gate->w.device != ctx->device || up->w.device != ctx->device) return DQ8_ERR_ARG;
+  DeviceGuard guard(ctx->device);
+  return gate_up(ctx, gate, up, q, scales, m, gate_bias, up_bias, nullptr, nullptr, h, nullptr, (hipStream_t)stream);
 }
 
 dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t m, const float* bias,
@@ -970,13 +1040,11 @@ dq8_status dq8_ffn(dq8_ctx* ctx, const dq8_ffn_weights* f, const int8_t* q, cons
   float* mid = (float*)((char*)ctx->chain + qbytes + sbytes);
   hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
   if (e != hipSuccess) return from_hip(e);
-  // gate: Write into h (qwen.rs:489); up: SwiGlu into h, quantized on the fly (qwen.rs:490-491)
-  dq8_linear_item gi = {f->gate, q, scales, m, f->gate_bias, h, DQ8_ROWS, DQ8_WRITE, f->gate_lora};
-  st = run_linear(ctx, &gi, 1, nullptr, s);
-  if (st != DQ8_OK) return st;
+  // gate: Write into h (qwen.rs:489); up: SwiGlu into h (qwen.rs:490); h is
+  // then quantized for down (qwen.rs:491).  Without adapters, on the wide
+  // kernel, both projections run in one launch that stores h directly.
   QOut qo = {qh, sh, ctx->flag};
-  dq8_linear_item ui = {f->up, q, scales, m, f->up_bias, h, DQ8_ROWS, DQ8_SWIGLU, f->up_lora};
-  st = run_linear(ctx, &ui, 1, nullptr, s, &qo);
+  st = gate_up(ctx, f->gate, f->up, q, scales, m, f->gate_bias, f->up_bias, f->gate_lora, f->up_lora, h, &qo, s);
   if (st != DQ8_OK) return st;
   if (nonfinite) {
     e = dq8::launch_or_u32(nonfinite, ctx->flag, s);

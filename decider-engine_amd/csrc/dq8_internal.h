@@ -49,6 +49,13 @@ struct Proj {
   int waves_n;        // column strips (skinny: skinny_cols(nseg) wide, wide: one block tile wide)
   int xcd_gm;         // wide: row bands of the per-XCD tile regions (1, 2, 4, 8), 0 = row-major order
   int nseg;           // skinny: waves per strip (1 or 4)
+  // Fused SwiGLU pair (wide kernel only): wt/wst/bias are the gate weights,
+  // wt2/wst2/bias2 the up weights of the same shape; the launch stores
+  // h = silu(gate(x) + bias) * (up(x) + bias2) into out [M][N].
+  const uint8_t* wt2;
+  const float* wst2;
+  const float* bias2;
+  int pair;
 };
 
 struct Batch {

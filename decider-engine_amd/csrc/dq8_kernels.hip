@@ -279,30 +279,30 @@ __device__ __forceinline__ void decode4(const void* base, size_t i, float (&v)[4
 }
 
 // Quantization: QuantizedInputs::new (tensor.rs:321-339) and the 8-bit
-// Data::quantize (weights.rs:117-136).  One wave covers 256 consecutive
-// elements of a row (4 per lane, 4 groups per wave); a group's absmax is a
-// max-reduction over its 16 lanes.  The division is the IEEE one and roundf
-// rounds half away from zero, as f32::round.  x holds DT elements; a
-// non-finite one ORs 1 into *nonfinite (Data::read rejects it for weights,
-// QuantizedInputs::new returns None for inputs).
+// Data::quantize (weights.rs:117-136).  A wave covers PER consecutive
+// 256-element chunks of one row (4 elements per lane and chunk, 4 groups per
+// chunk); every chunk's load is issued before the first is used, so a wave
+// keeps PER KB (fp32) in flight.  A group's absmax is a max-reduction over its
+// 16 lanes.  The division is the IEEE one and roundf rounds half away from
+// zero, as f32::round.  x holds DT elements; a non-finite one ORs 1 into
+// *nonfinite (Data::read rejects it for weights, QuantizedInputs::new returns
+// None for inputs).  The host guarantees rows * ceil(chunks / PER) < 2^31.
 template <int DT, int PER>
 __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, int rows, int k, int8_t* __restrict__ q,
                                                   int ldq, float* __restrict__ scales, int lds, uint32_t* nonfinite) {
-  constexpr int ES = DT == kDtypeF32 ? 4 : 2;  // element bytes
   const int lane = threadIdx.x & 63;
   const int chunks = (k + 255) >> 8;
-  const long total = (long)rows * chunks;
-  // PER consecutive 256-element chunks per wave, all loaded before any is used
-  const long first = ((long)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * PER;
-  if (first >= total) return;  // wave-uniform
-  const bool vec = (k & 3) == 0 && ((uintptr_t)x & (4 * ES - 1)) == 0;
+  const int wpr = (chunks + PER - 1) / PER;  // waves per row
+  const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row = wave / wpr;
+  if (row >= rows) return;  // wave-uniform
+  const int c0 = (wave - row * wpr) * PER;
+  const bool vec = (k & 3) == 0 && ((uintptr_t)x & (DT == kDtypeF32 ? 15 : 7)) == 0;
+  const size_t r0 = (size_t)row * k;
   float v[PER][4];
 #pragma unroll
   for (int p = 0; p < PER; ++p) {
-    const long item = min(first + p, total - 1);  // past the end: recomputes the last chunk, not stored
-    const int row = (int)(item / chunks), chunk = (int)(item - (long)row * chunks);
-    const int k0 = chunk * 256 + lane * 4;
-    const size_t r0 = (size_t)row * k;
+    const int k0 = (c0 + p) * 256 + lane * 4;  // chunks past the row's end: k0 >= k, all zeros, not stored
     if (vec && k0 + 3 < k) {
       decode4<DT>(x, r0 + k0, v[p]);
     } else {
@@ -310,20 +310,21 @@ __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, in
       for (int i = 0; i < 4; ++i) v[p][i] = (k0 + i < k) ? decode<DT>(x, r0 + k0 + i) : 0.0f;
     }
   }
+  int8_t* qr = q + (size_t)row * ldq;
+  const bool qvec = (ldq & 3) == 0 && ((uintptr_t)q & 3) == 0;
+  const int groups = (k + kGroup - 1) / kGroup;
+  bool bad = false;
 #pragma unroll
   for (int p = 0; p < PER; ++p) {
-    const long item = first + p;
-    if (item >= total) break;  // wave-uniform
-    const int row = (int)(item / chunks), chunk = (int)(item - (long)row * chunks);
+    const int chunk = c0 + p;
+    if (chunk >= chunks) break;  // wave-uniform
     const int k0 = chunk * 256 + lane * 4;
-    bool bad = false;
     float m = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       bad |= !isfinite(v[p][i]);
       m = fmaxf(m, fabsf(v[p][i]));
     }
-    if (bad && nonfinite) atomicOr(nonfinite, 1u);
     // max over the 16 lanes of this group (fmaxf of non-negative values is order-free)
     m = fmaxf(m, __shfl_xor(m, 1));
     m = fmaxf(m, __shfl_xor(m, 2));
@@ -345,8 +346,7 @@ __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, in
       r = fminf(fmaxf(r, -127.0f), 127.0f);
       packed |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * i);
     }
-    int8_t* qr = q + (size_t)row * ldq;
-    if ((ldq & 3) == 0 && k0 + 3 < ldq && ((uintptr_t)q & 3) == 0) {
+    if (qvec && k0 + 3 < ldq) {
       // Padding bytes [k, ldq) are written as zero (v = 0 there).
       *reinterpret_cast<uint32_t*>(qr + k0) = packed;
     } else {
@@ -354,9 +354,12 @@ __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, in
       for (int i = 0; i < 4; ++i)
         if (k0 + i < ldq) qr[k0 + i] = (int8_t)(packed >> (8 * i));
     }
-    const int group = (chunk * 256 + (lane & ~15) * 4) / kGroup;
-    const int groups = (k + kGroup - 1) / kGroup;
+    const int group = chunk * 4 + (lane >> 4);
     if ((lane & 15) == 0 && group < groups) scales[(size_t)row * lds + group] = scale;
+  }
+  if (nonfinite) {  // one atomic per wave that saw a non-finite element
+    const unsigned long long b = __ballot(bad);
+    if (b != 0 && lane == __builtin_ffsll((long long)b) - 1) atomicOr(nonfinite, 1u);
   }
 }
 
@@ -512,7 +515,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 #endif
 // 256-element chunks per wave of the quantizer.
 #ifndef DQ8_QUANT_PER
-#define DQ8_QUANT_PER 1
+#define DQ8_QUANT_PER 4
 #endif
 // Launches of at most this many blocks (three times as many when they mix
 // long and short K) use a ring of STAGES + 1 groups.
@@ -597,7 +600,12 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   const Proj P = b.p[find_proj(b, blk)];
   int mt, nt;
   tile_of(P, blk - P.wave_begin, (P.m + BM - 1) / BM, mt, nt);
-  const int m0 = mt * BM, n0 = nt * BN;
+  // A SwiGLU pair block covers BN/2 output columns: wave wn's column tile 0
+  // is the gate projection's, tile 1 the up projection's, of the same 32
+  // outputs (RT == 1, CT == 2 only).
+  constexpr bool CAN_PAIR = !DOTS && !LORA && RT == 1 && CT == 2 && WN == 2;
+  const bool pair = CAN_PAIR && P.pair;
+  const int m0 = mt * BM, n0 = nt * (pair ? BN / 2 : BN);
   const int G = P.g;
   auto swz = [](int r) { return SWZ == 0 ? (r >> 2) & 3 : (r >> 1) & 3; };
 
@@ -617,6 +625,13 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       sbase[k] = reinterpret_cast<const uint8_t*>(P.q) + (size_t)r0 * P.ldq;
       loff[k] = (uint32_t)((row - r0) * P.ldq + 16 * ((lane & 3) ^ swz(rr)));
       stride[k] = kGroup;
+    } else if (pair) {
+      // fragment fb: column tile ct = fb/2 of the block is tile ct%2 (gate or
+      // up) of wave ct/2, output columns n0 + 32*(ct/2) ..
+      const int fb = i - AS, ct = fb >> 1;
+      sbase[k] = ((ct & 1) ? P.wt2 : P.wt) + ((size_t)(n0 / 32 + (ct >> 1)) * G * 2 + (fb & 1)) * kFragBytes;
+      loff[k] = (uint32_t)lane * 16;
+      stride[k] = 2 * kFragBytes;
     } else {
       const int fb = i - AS;
       sbase[k] = P.wt + ((size_t)(n0 / 32 + (fb >> 1)) * G * 2 + (fb & 1)) * kFragBytes;
@@ -626,8 +641,10 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   }
   // w scales: wave w < WSD loads columns 64w .. 64w+63; the others repeat wave
   // w % WSD's load (same data, same place).  Row G of the scales is zero.
+  // (SwiGLU pair: wave 0 loads the gate scales of the block's 64 outputs,
+  // wave 1 the up scales, to ws[0..63] and ws[64..127].)
   const int ww = WSD > 0 ? wid % (WSD > 0 ? WSD : 1) : 0;
-  const float* wsbase = P.wst + n0 + 64 * ww;
+  const float* wsbase = pair ? (ww ? P.wst2 : P.wst) + n0 : P.wst + n0 + 64 * ww;
   // x-scale pieces: load d = k*NW + wid of a chunk covers rows RPD*d .. RPD*d+RPD-1;
   // lane l fetches row l/PPR, piece (l%PPR) ^ (row%PPR).
 
@@ -742,7 +759,8 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
         for (int j = 0; j < NP; ++j) {
           const v16i& lo = RT == 2 ? dt[0][j] : dt[0][0];
           const v16i& hi = RT == 2 ? dt[1][j] : dt[0][1];
-          const float w = RT == 2 ? cur.ws[WC * wn + 32 * j + (lane & 31)] : cur.ws[WC * wn + lane];
+          const float w = RT == 2 ? cur.ws[WC * wn + 32 * j + (lane & 31)]
+                          : cur.ws[pair ? 64 * (lane >> 5) + 32 * wn + (lane & 31) : WC * wn + lane];
           const v32f dv = mfma_k1(-kMagic, 1.0f, concat(lo, hi));
           const v32f pv = mfma_k1(x, w, zero32);
           s[j] = s[j] + dv * pv;
@@ -752,6 +770,26 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   }
   // Drain the clamped loads of the groups past the end before the block exits.
   wait_vmcnt<0>();
+  if constexpr (CAN_PAIR) {
+    if (pair) {
+      // y = s + bias for both projections (tensor.rs:437), then the up
+      // projection's SwiGlu store over the gate's result (tensor.rs:96-99,
+      // qwen.rs:489-490): h = silu(y_gate) * y_up, each op rounded.
+      const int mw = m0 + WR * wm, col = n0 + 32 * wn + (lane & 31);
+      const float bg = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
+      const float bu = P.bias2 != nullptr && col < P.n ? P.bias2[col] : 0.0f;
+      const ExpTab T = exp_table(lane);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = mw + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        const float yg = s[0][v] + bg, yu = s[0][16 + v] + bu;
+        const float h = silu_wave(yg, T) * yu;
+        if (row < P.m && col < P.n) P.out[(size_t)row * P.n + col] = h;
+        if ((v & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+      return;
+    }
+  }
   if constexpr (!DOTS) {
     const int mw = m0 + WR * wm, nw = n0 + WC * wn;
     // y = s + bias[col], or s + 0.0f without a bias (tensor.rs:437)
@@ -1845,9 +1883,10 @@ hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int ran
 hipError_t launch_quantize_raw(const void* x, int dtype, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
                                uint32_t* nonfinite, hipStream_t s) {
   constexpr int PER = DQ8_QUANT_PER;
-  const long items = (long)rows * ((k + 255) / 256);
-  if (items == 0) return hipSuccess;
-  const int blocks = blocks_for(blocks_for(items, PER), 4);
+  const long waves = (long)rows * (((k + 255) / 256 + PER - 1) / PER);
+  if (waves == 0) return hipSuccess;
+  if (waves >= (1L << 31) - 4) return hipErrorInvalidValue;
+  const int blocks = blocks_for(waves, 4);
   if (dtype == kDtypeBF16)
     k_quantize<kDtypeBF16, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
   else if (dtype == kDtypeF16)

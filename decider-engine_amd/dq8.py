@@ -130,6 +130,7 @@ def lib() -> ctypes.CDLL:
         "dq8_linear_lora": ([_vp, _vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
         "dq8_linear_q": ([_vp, _vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _vp, _vp, _vp, _vp], _i),
         "dq8_ffn": ([_vp, ctypes.POINTER(_FfnWeights), _vp, _vp, _sz, _vp, _vp, _vp, _vp], _i),
+        "dq8_ffn_gate_up": ([_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp], _i),
         "dq8_group_dots": ([_vp, _vp, _vp, _sz, _vp, _vp], _i),
         "dq8_status_string": ([_i], ctypes.c_char_p),
         "dq8_linear_fp32": ([_vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
@@ -483,6 +484,21 @@ class Context:
                 a.shape[0], sc
         _check(lib().dq8_ffn(self.handle, ctypes.byref(fw), q.data_ptr(), scales.data_ptr(), m, h.data_ptr(),
                              residual.data_ptr(), _ptr(nonfinite), _stream(self.device)), "dq8_ffn")
+        return h
+
+    def ffn_gate_up(self, gate: Weights, up: Weights, q, scales, h=None, biases=(None, None)):
+        """h = silu(gate(x) + gate_bias) * (up(x) + up_bias) (qwen.rs:489-490), the gate Write and up SwiGlu
+        stores of one FFN in one call.  Returns h [m][n]."""
+        torch = _torch()
+        self._dev(q, torch.int8, name="q")
+        m, k = q.shape
+        self._dev(scales, torch.float32, (m, groups(k)), "scales")
+        if h is None:
+            h = torch.empty((m, up.n), dtype=torch.float32, device=self.device)
+        self._dev(h, torch.float32, (m, up.n), "h")
+        _check(lib().dq8_ffn_gate_up(self.handle, gate.handle, up.handle, q.data_ptr(), scales.data_ptr(), m,
+                                     _ptr(biases[0]), _ptr(biases[1]), h.data_ptr(), _stream(self.device)),
+               "dq8_ffn_gate_up")
         return h
 
     def linear_f32in(self, w: Weights, x, out=None, bias=None, layout=ROWS, epilogue=WRITE):

@@ -227,6 +227,18 @@ typedef struct dq8_ffn_weights {
     size_t down_lora_rank;
     float down_lora_scale;
 } dq8_ffn_weights;
+/* The FFN's gate and up projections (qwen.rs:489-490) on one shared quantized
+ * input: h = silu(gate(x) + gate_bias) * (up(x) + up_bias), exactly what
+ * dq8_linear(gate, DQ8_WRITE into h) followed by dq8_linear(up, DQ8_SWIGLU
+ * into h) store, bit for bit (Epilogue::SwiGlu, tensor.rs:96-99).  With more
+ * than 64 rows both projections run in one launch that computes a gate and an
+ * up tile of the same outputs side by side, so h is stored once and the gate
+ * result is never written and read back.  No reference counterpart of its own:
+ * it schedules the crate's two apply calls of the FFN together.  gate and up
+ * must have the same shape; h is [m][n] (rows layout). */
+dq8_status dq8_ffn_gate_up(dq8_ctx *ctx, const dq8_weights *gate, const dq8_weights *up, const int8_t *q,
+                           const float *scales, size_t m, const float *gate_bias, const float *up_bias, float *h,
+                           void *stream);
 /* One layer's FFN chain on the device (qwen.rs:486-492):
  *   h = gate(x)                          Write            (Linear::apply_shared)
  *   h = silu(h) * up(x)                  SwiGlu           (apply_into_shared)

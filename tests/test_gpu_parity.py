@@ -782,7 +782,7 @@ def test_linear_q_reports_nonfinite_results(ctx):
 
 
 @pytest.mark.parametrize("m,hidden,inter,lora", [(130, 256, 384, False), (24, 256, 384, True), (512, 2048, 6144, False),
-                                                 (96, 192, 320, True)])
+                                                 (96, 192, 320, True), (200, 256, 300, False), (65, 512, 128, False)])
 def test_ffn_chain_matches_the_reference_sequence(ctx, m, hidden, inter, lora):
     # qwen.rs:486-492: h = silu(gate(x)) * up(x); residual += down(h), with h
     # re-quantized per token.  h and the residual are both bit-exact.
@@ -815,6 +815,57 @@ def test_ffn_chain_matches_the_reference_sequence(ctx, m, hidden, inter, lora):
         want_r = dq8o.linear(want_h, dv, ds, result=resid0, epilogue=1, threads=8)
     assert bits_equal(h, want_h)
     assert bits_equal(host(resid), want_r)
+
+
+@pytest.mark.parametrize("m,hidden,inter", [(130, 256, 384), (40, 256, 384), (24, 128, 96), (300, 1024, 520),
+                                             (1000, 2048, 2048)])
+def test_ffn_gate_up_equals_write_then_swiglu(ctx, m, hidden, inter):
+    # dq8_ffn_gate_up stores what the crate's gate Write and up SwiGlu apply
+    # calls store (qwen.rs:489-490): the same bits as two dq8_linear calls and as
+    # the oracle, with and without biases; more than 64 rows take the one-launch
+    # pair path, fewer the two launches.
+    rng = np.random.default_rng(m * 7 + inter)
+    x = make_x(rng, m, hidden, "outliers")
+    gv, gs = dq8o.quantize_weights(make_w(rng, inter, hidden))
+    uv, us = dq8o.quantize_weights(make_w(rng, inter, hidden))
+    G, U = ctx.weights_from_quantized(dev(gv), dev(gs)), ctx.weights_from_quantized(dev(uv), dev(us))
+    q, s = ctx.quantize(dev(x))
+    gb = (rng.standard_normal(inter) * 0.5).astype(np.float32)
+    ub = (rng.standard_normal(inter) * 0.5).astype(np.float32)
+    for biases in ((None, None), (gb, ub), (None, ub)):
+        db = tuple(None if b is None else dev(b) for b in biases)
+        got = host(ctx.ffn_gate_up(G, U, q, s, biases=db))
+        h = ctx.linear(G, q, s, bias=db[0])
+        ctx.linear(U, q, s, out=h, bias=db[1], epilogue=dq8.SWIGLU)
+        assert bits_equal(got, host(h))
+        gate = dq8o.linear(x, gv, gs, bias=biases[0], threads=8)
+        assert bits_equal(got, dq8o.linear(x, uv, us, bias=biases[1], result=gate, epilogue=2, threads=8))
+
+
+@pytest.mark.parametrize("kind", ["student", "edge"])
+def test_ffn_full_size_sampled_rows(ctx, kind):
+    # One FFN of the 24-layer stack at full size: 2048 tokens, 2048 -> 6144
+    # gate/up (one launch of 3072 blocks storing h), h re-quantized, 6144 ->
+    # 2048 down Add (qwen.rs:486-492).  Rows are independent, so the oracle
+    # recomputes 24 sampled rows of h and of the residual.
+    rng = np.random.default_rng(6144 + len(kind))
+    m, hidden, inter = 2048, 2048, 6144
+    x = make_x(rng, m, hidden, kind)
+    gv, gs = dq8o.quantize_weights(make_w(rng, inter, hidden))
+    uv, us = dq8o.quantize_weights(make_w(rng, inter, hidden))
+    dv, ds = dq8o.quantize_weights(make_w(rng, hidden, inter))
+    gb = (rng.standard_normal(inter) * 0.1).astype(np.float32)
+    G, U, D = (ctx.weights_from_quantized(dev(v), dev(s)) for v, s in ((gv, gs), (uv, us), (dv, ds)))
+    q, s = ctx.quantize(dev(x))
+    resid0 = rng.standard_normal((m, hidden)).astype(np.float32)
+    resid = dev(resid0.copy())
+    h = host(ctx.ffn(G, U, D, q, s, resid, biases=(dev(gb), None, None)))
+    rows = np.unique(np.r_[0, m - 1, rng.choice(m, size=22, replace=False)])
+    gate = dq8o.linear(x[rows], gv, gs, bias=gb, threads=8)
+    want_h = dq8o.linear(x[rows], uv, us, result=gate, epilogue=2, threads=8)
+    assert bits_equal(h[rows], want_h)
+    want_r = dq8o.linear(want_h, dv, ds, result=resid0[rows], epilogue=1, threads=8)
+    assert bits_equal(host(resid)[rows], want_r)
 
 
 def test_full_size_gdn_in_projection_properties(ctx):
