@@ -515,7 +515,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 #endif
 // 256-element chunks per wave of the quantizer.
 #ifndef DQ8_QUANT_PER
-#define DQ8_QUANT_PER 4
+#define DQ8_QUANT_PER 1
 #endif
 // Launches of at most this many blocks (three times as many when they mix
 // long and short K) use a ring of STAGES + 1 groups.
