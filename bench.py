@@ -66,6 +66,8 @@ def parse():
     p.add_argument("--weight-copies", type=int, default=5)
     p.add_argument("--skinny-reps", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--stack-only", action="store_true",
+                   help="time the headline stack only (no other legs, no CPU baseline): for kernel profiles")
     p.add_argument("--no-graph", action="store_true", help="time eager submission only (no HIP graph replay)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--lora-rank", type=int, default=16,
@@ -324,7 +326,10 @@ def main():
     lin_avg_ms = lin_ms / lin_n
     achieved = lin_ops_per_launch / (lin_avg_ms * 1e-3) / 1e12
     value = step_ops / (ms_step * 1e-3) / 1e12
-    lora = run_lora_stack(args, torch, stream, build, run_step, step_ops, ms_step) if rank > 0 else None
+    if args.stack_only:
+        args.no_cpu_baseline = True
+    lora = run_lora_stack(args, torch, stream, build, run_step, step_ops, ms_step) \
+        if rank > 0 and not args.stack_only else None
     # outputs of the first (GDN) and last (GQA) layer of the timed step, run once more on their own from a zero
     # residual, kept for the oracle check of the cpu_baseline leg
     stack_checks = [capture_layer(torch, dq8, layers, calls[bounds[i]:bounds[i + 1]], i, M, bufs)
@@ -340,14 +345,16 @@ def main():
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
 
-    stacked, skinny = run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen)
-    load = run_load(args, torch, dq8, ctx, gen)
-    keep_checks = not args.no_cpu_baseline
-    config1 = run_config1(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
-    config2 = run_config2(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
-    config3 = run_config3(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
-    reference = run_reference_benchmarks(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
-    round_trip = run_host_round_trip(args, torch, dq8, ctx, lib, dev, stream)
+    stacked = skinny = load = config1 = config2 = config3 = reference = round_trip = None
+    if not args.stack_only:
+        stacked, skinny = run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen)
+        load = run_load(args, torch, dq8, ctx, gen)
+        keep_checks = not args.no_cpu_baseline
+        config1 = run_config1(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
+        config2 = run_config2(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
+        config3 = run_config3(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
+        reference = run_reference_benchmarks(args, torch, dq8, ctx, lib, dev, stream, keep_checks)
+        round_trip = run_host_round_trip(args, torch, dq8, ctx, lib, dev, stream)
     cpu = None
     if not args.no_cpu_baseline:
         checks = {"stack_layer_0": stack_checks[0], "stack_layer_23": stack_checks[1],

@@ -199,6 +199,34 @@ int xcd_rows_split(int row_tiles, int col_tiles, size_t a_bytes, size_t b_bytes)
   return best;
 }
 
+// Blocks of one launch that an XCD runs at the same time (32 CUs x 4 blocks).
+#ifndef DQ8_XCD_SLOTS
+#define DQ8_XCD_SLOTS 128
+#endif
+// Walk order within an XCD's region (tile_of): bands of sr row tiles, each in
+// chunks of sc column tiles.  A chunk of about DQ8_XCD_SLOTS tiles runs at
+// once; pick the sr (a divisor of the region's row tiles) whose chunk touches
+// the fewest operand bytes: sr row tiles of activations plus sc column tiles
+// of weights (a column tile of a SwiGLU pair holds both projections' rows).
+void xcd_chunks(dq8::Proj& p, int row_tiles) {
+  p.xcd_sr = 1;
+  p.xcd_sc = 1;
+  if (p.xcd_gm == 0) return;
+  const int rm = row_tiles / p.xcd_gm, rn = p.waves_n / (8 / p.xcd_gm);
+  const double a_tile = (double)dq8::wide_block_rows(), b_tile = (double)dq8::wide_block_cols();
+  double best = -1.0;
+  for (int sr = 1; sr <= rm; ++sr) {
+    if (rm % sr) continue;
+    const int sc = std::min(rn, std::max(1, (DQ8_XCD_SLOTS + sr - 1) / sr));
+    const double cost = (sr * a_tile + sc * b_tile) / ((double)sr * sc);  // operand rows per tile
+    if (best < 0 || cost < best) {
+      best = cost;
+      p.xcd_sr = sr;
+      p.xcd_sc = sc;
+    }
+  }
+}
+
 // Kernel kind of a projection (see launch_linear).
 int kind_of(const dq8::Weights&, size_t m) { return m > 32 ? 0 : m > 16 ? 2 : 1; }
 
@@ -223,6 +251,7 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips) {
                        : p.np / dq8::wide_block_cols();
     const int row_tiles = (p.m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows();
     p.xcd_gm = xcd_rows_split(row_tiles, p.waves_n, (size_t)p.m * p.g, (size_t)(p.pair ? 2 : 1) * p.n * p.g);
+    xcd_chunks(p, row_tiles);
     b.total_waves += p.waves_n * row_tiles;
   } else {
     p.nseg = dq8::skinny_segments(p.g, few_strips);

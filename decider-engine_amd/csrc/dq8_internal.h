@@ -48,6 +48,7 @@ struct Proj {
   int wave_begin;     // first block of this projection in the launch
   int waves_n;        // column strips (skinny: skinny_cols(nseg) wide, wide: one block tile wide)
   int xcd_gm;         // wide: row bands of the per-XCD tile regions (1, 2, 4, 8), 0 = row-major order
+  int xcd_sr, xcd_sc; // wide: a region is walked in chunks of xcd_sr row tiles x xcd_sc column tiles
   int nseg;           // skinny: waves per strip (1 or 4)
   // Fused SwiGLU pair (wide kernel only): wt/wst/bias are the gate weights,
   // wt2/wst2/bias2 the up weights of the same shape; the launch stores

@@ -431,9 +431,13 @@ __global__ void k_pad_rows(const int8_t* __restrict__ q, int rows, int k, int8_t
 // Tile (row tile mt, column tile nt) of block i of a projection.  Blocks are
 // dealt to the 8 XCDs round robin, so blocks i, i+8, ... share one XCD and its
 // L2.  With P.xcd_gm = gm the tile grid is cut into gm x (8/gm) regions and
-// XCD i%8 walks region i%8, column tiles fastest: it touches 1/gm of the
-// activation rows and 1/(8/gm) of the weight columns.  The map is a bijection
-// on [0, row_tiles * col_tiles) (the host picks gm dividing both counts).
+// XCD i%8 walks region i%8: it touches 1/gm of the activation rows and
+// 1/(8/gm) of the weight columns.  Within its region an XCD takes bands of
+// sr = P.xcd_sr row tiles, and each band in chunks of sc = P.xcd_sc column
+// tiles, row tiles fastest, so the blocks that run at the same time share sr
+// row tiles of activations and sc column tiles of weights in L2.  The map is a
+// bijection on [0, row_tiles * col_tiles) (the host picks gm dividing both
+// counts and sr dividing the region's row tiles).
 __device__ __forceinline__ void tile_of(const Proj& P, int i, int row_tiles, int& mt, int& nt) {
   const int col_tiles = P.waves_n;
   if (P.xcd_gm == 0) {
@@ -445,9 +449,12 @@ __device__ __forceinline__ void tile_of(const Proj& P, int i, int row_tiles, int
   const int rm = row_tiles / gm, rn = col_tiles / gn;  // region size in tiles
   const int x = i & 7, j = i >> 3;
   const int xa = x / gn, xb = x - xa * gn;
-  const int lm = j / rn;
-  mt = xa * rm + lm;
-  nt = xb * rn + (j - lm * rn);
+  const int sr = P.xcd_sr, sc = P.xcd_sc;
+  const int band = j / (sr * rn), t = j - band * (sr * rn);
+  const int chunk = t / (sr * sc), u = t - chunk * (sr * sc);
+  const int ur = u % sr;
+  mt = xa * rm + band * sr + ur;
+  nt = xb * rn + chunk * sc + (u - ur) / sr;
 }
 
 // Direct global->LDS loads.  They are issued through inline assembly so the
