@@ -66,8 +66,8 @@ def parse():
     p.add_argument("--weight-copies", type=int, default=5)
     p.add_argument("--skinny-reps", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--stack-only", action="store_true",
-                   help="time the headline stack only (no other legs, no CPU baseline): for kernel profiles")
+    p.add_argument("--only", choices=["stack", "skinny"],
+                   help="run one leg only (no CPU baseline) and print its figures: for kernel profiles")
     p.add_argument("--no-graph", action="store_true", help="time eager submission only (no HIP graph replay)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--lora-rank", type=int, default=16,
@@ -111,6 +111,11 @@ def main():
     sh = stream.cuda_stream
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
+    if args.only == "skinny":
+        args.no_cpu_baseline = True
+        stacked, skinny = run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen)
+        print(json.dumps({"skinny": skinny, "questions_stacked": stacked}))
+        return
 
     def weights(n, k):
         w = (torch.randn((n, k), generator=gen, device=dev) * 0.02).contiguous()
@@ -326,10 +331,10 @@ def main():
     lin_avg_ms = lin_ms / lin_n
     achieved = lin_ops_per_launch / (lin_avg_ms * 1e-3) / 1e12
     value = step_ops / (ms_step * 1e-3) / 1e12
-    if args.stack_only:
+    if args.only == "stack":
         args.no_cpu_baseline = True
     lora = run_lora_stack(args, torch, stream, build, run_step, step_ops, ms_step) \
-        if rank > 0 and not args.stack_only else None
+        if rank > 0 and args.only is None else None
     # outputs of the first (GDN) and last (GQA) layer of the timed step, run once more on their own from a zero
     # residual, kept for the oracle check of the cpu_baseline leg
     stack_checks = [capture_layer(torch, dq8, layers, calls[bounds[i]:bounds[i + 1]], i, M, bufs)
@@ -346,7 +351,7 @@ def main():
     torch.cuda.empty_cache()
 
     stacked = skinny = load = config1 = config2 = config3 = reference = round_trip = None
-    if not args.stack_only:
+    if args.only is None:
         stacked, skinny = run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen)
         load = run_load(args, torch, dq8, ctx, gen)
         keep_checks = not args.no_cpu_baseline

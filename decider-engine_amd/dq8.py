@@ -23,7 +23,8 @@ import re
 from dataclasses import dataclass
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libdq8.so")
+# DQ8_LIBRARY selects another build of the library (for comparing kernel variants)
+LIB_PATH = os.environ.get("DQ8_LIBRARY") or os.path.join(_HERE, "libdq8.so")
 HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "dq8.h")
 
 OK, ERR_SHAPE, ERR_NONFINITE, ERR_ARG, ERR_DEVICE, ERR_NOMEM, ERR_FORMAT, ERR_IO, ERR_CAPTURE, ERR_LIMIT = range(10)
