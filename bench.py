@@ -253,12 +253,13 @@ def main():
                 calls.append(quant(gate, qf, sf, FFN_DIM))
                 proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
             else:
-                # gate and up in one launch storing h (qwen.rs:489-490), h re-quantized, down Add
+                # gate and up in one launch storing h and its quantization for down (qwen.rs:489-491),
+                # then down Add
                 ops = sum(2 * M * L[n].n * L[n].k for n in ("gate", "up"))
                 calls.append(("linear", lib.dq8_ffn_gate_up, (ctx.handle, L["gate"].handle, L["up"].handle,
                                                               qx.data_ptr(), sx.data_ptr(), M, None, None,
-                                                              gate.data_ptr(), sh), (0, ops)))
-                calls.append(quant(gate, qf, sf, FFN_DIM))
+                                                              gate.data_ptr(), qf.data_ptr(), sf.data_ptr(),
+                                                              flag.data_ptr(), sh), (0, ops)))
                 proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
         layer_bounds.append(len(calls))
         return calls
@@ -789,7 +790,7 @@ def ok(st, what):
 
 def capture_layer(torch, dq8, layers, calls, i, M, bufs):
     """Layer i of the stack (its calls of the timed step: quantize, in / q,k,v, quantize, out / o, quantize,
-    the FFN chain: gate and up (SwiGlu) storing h, h re-quantized, down (Add)) run once more from a zero
+    the FFN chain: gate and up (SwiGlu) storing h and its quantization, down (Add)) run once more from a zero
     residual; sampled rows of its inputs, outputs and weights are kept for the oracle."""
     L = layers[i]
     bufs["resid"].zero_()

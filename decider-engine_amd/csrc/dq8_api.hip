@@ -176,6 +176,9 @@ void fill_proj(dq8::Proj& p, const dq8::Weights& w, const int8_t* q, int ldq, co
   p.wt2 = nullptr;
   p.wst2 = nullptr;
   p.bias2 = nullptr;
+  p.hq = nullptr;
+  p.hs = nullptr;
+  p.hflag = nullptr;
   p.pair = 0;
 }
 
@@ -304,8 +307,8 @@ struct QOut {
 
 // Split items by kernel kind and launch.  Items with m == 0 do nothing (tensor.rs:152-154).
 // qout (one item only): the item's stored result is then quantized by k_quantize.
-// (Quantizing in the projection's epilogue was measured slower: the projection
-// kernels are VALU-bound, the quantize pass is memory-bound.)
+// (Only the SwiGLU pair launch, run_pair, quantizes its result in its own
+// epilogue; the step's other quantized inputs come from outside the projections.)
 // unless: the launches do nothing on the device if *unless != 0 (the inputs
 // were not finite; the caller runs the FP32 kernel for these items).
 dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, int32_t* dots, hipStream_t s,
@@ -411,9 +414,11 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
 
 // One layer's gate and up projections (same shape, shared quantized input,
 // no adapters) in one wide launch that stores h = silu(gate + bias) * (up +
-// bias2) into h [m][n], then quantizes h as qout asks.  The results equal the
-// separate Write and SwiGlu launches bit for bit: each output's arithmetic is
-// unchanged, only the two tiles of one output sit in one wave.
+// bias2) into h [m][n] and, as qout asks, quantizes h in the same launch
+// (q [m][n], scales [m][ceil(n/64)], the non-finite flag).  The results equal
+// the separate Write and SwiGlu launches and k_quantize bit for bit: each
+// output's arithmetic is unchanged, only the two tiles of one output sit in
+// one wave, and a block holds whole 64-column groups of h.
 dq8_status run_pair(dq8_ctx* ctx, const dq8::Weights& g, const dq8::Weights& u, const int8_t* q, const float* xs,
                     size_t m, const float* gate_bias, const float* up_bias, float* h, const QOut* qout,
                     hipStream_t s) {
@@ -428,16 +433,14 @@ dq8_status run_pair(dq8_ctx* ctx, const dq8::Weights& g, const dq8::Weights& u, 
   p.wt2 = u.values;
   p.wst2 = u.scales;
   p.bias2 = up_bias;
+  if (qout) {
+    p.hq = qout->q;
+    p.hs = qout->scales;
+    p.hflag = qout->nonfinite;
+  }
   p.pair = 1;
   place_proj(p, 0, b, false);
-  hipError_t e = dq8::launch_linear(b, 0, false, s);
-  if (e != hipSuccess) return from_hip(e);
-  if (qout) {
-    e = dq8::launch_quantize(h, (int)m, g.n, qout->q, g.n, qout->scales, (g.n + kGroup - 1) / kGroup,
-                             qout->nonfinite, s);
-    if (e != hipSuccess) return from_hip(e);
-  }
-  return DQ8_OK;
+  return from_hip(dq8::launch_linear(b, 0, false, s));
 }
 
 // ------------------------------------------------------- fp32-input paths
@@ -957,15 +960,25 @@ dq8_status dq8_linear_batch(dq8_ctx* ctx, const dq8_linear_item* items, size_t c
 
 dq8_status dq8_ffn_gate_up(dq8_ctx* ctx, const dq8_weights* gate, const dq8_weights* up, const int8_t* q,
                            const float* scales, size_t m, const float* gate_bias, const float* up_bias, float* h,
-                           void* stream) {
+                           int8_t* h_q, float* h_scales, uint32_t* nonfinite, void* stream) {
   if (!ctx || !gate || !up) return DQ8_ERR_ARG;
   if (m == 0) return DQ8_OK;
   if (gate->w.k != up->w.k || gate->w.n != up->w.n) return DQ8_ERR_SHAPE;
   dq8_status st = check_item_args(gate, q, scales, m, h, DQ8_ROWS, DQ8_WRITE);
   if (st != DQ8_OK) return st;
   if (gate->w.device != ctx->device || up->w.device != ctx->device) return DQ8_ERR_ARG;
+  if ((h_q == nullptr) != (h_scales == nullptr)) return DQ8_ERR_ARG;
   DeviceGuard guard(ctx->device);
-  return gate_up(ctx, gate, up, q, scales, m, gate_bias, up_bias, nullptr, nullptr, h, nullptr, (hipStream_t)stream);
+  hipStream_t s = (hipStream_t)stream;
+  if (!h_q) return gate_up(ctx, gate, up, q, scales, m, gate_bias, up_bias, nullptr, nullptr, h, nullptr, s);
+  if (!nonfinite) {
+    hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
+    if (e != hipSuccess) return from_hip(e);
+  }
+  QOut qo = {h_q, h_scales, nonfinite ? nonfinite : ctx->flag};
+  st = gate_up(ctx, gate, up, q, scales, m, gate_bias, up_bias, nullptr, nullptr, h, &qo, s);
+  if (st != DQ8_OK || nonfinite) return st;
+  return finish_nonfinite(ctx, s);
 }
 
 dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t m, const float* bias,

@@ -52,10 +52,15 @@ struct Proj {
   int nseg;           // skinny: waves per strip (1 or 4)
   // Fused SwiGLU pair (wide kernel only): wt/wst/bias are the gate weights,
   // wt2/wst2/bias2 the up weights of the same shape; the launch stores
-  // h = silu(gate(x) + bias) * (up(x) + bias2) into out [M][N].
+  // h = silu(gate(x) + bias) * (up(x) + bias2) into out [M][N].  With hq
+  // set it also quantizes h as k_quantize does: hq [M][N] int8, hs [M][G_h]
+  // scales (G_h = ceil(N / 64)), 1 ORed into *hflag if h is not finite.
   const uint8_t* wt2;
   const float* wst2;
   const float* bias2;
+  int8_t* hq;
+  float* hs;
+  uint32_t* hflag;
   int pair;
 };
 

@@ -278,13 +278,52 @@ __device__ __forceinline__ void decode4(const void* base, size_t i, float (&v)[4
   }
 }
 
+// One group's scale from its absmax m (weights.rs:117-136): absmax / 127, at
+// least FLT_MIN, 1 for an all-zero group.
+__device__ __forceinline__ float quant_scale(float m) {
+  return (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
+}
+// N elements of one group: round(v / scale) half away from zero (f32::round of
+// the IEEE quotient), clamped to [-127, 127], packed 4 bytes to a word.
+// The quotient is taken through rs = rcp(scale) (1 ulp): a = v * rs differs from
+// the IEEE quotient Q by less than 2^-15 (|Q| <= 127, relative error < 2^-22).
+// t = a + copysign(0.5, a) is within 2^-18 of a + sign * 0.5, so when t lies
+// more than 2^-14 from every integer, trunc(t) is round(Q); a lane with an
+// element closer than that (about 1 in 8000 elements) divides all N exactly.
+template <int N>
+__device__ __forceinline__ void quant_pack(const float (&v)[N], float scale, uint32_t (&w)[N / 4]) {
+  const float rs = __builtin_amdgcn_rcpf(scale);
+  float r[N];
+  float d = 1.0f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float a = v[i] * rs;
+    const float t = a + copysignf(0.5f, a);
+    r[i] = truncf(t);
+    d = fminf(d, fabsf(t - rintf(t)));
+  }
+  if (!(d > 0x1p-14f)) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) r[i] = roundf(v[i] / scale);
+  }
+#pragma unroll
+  for (int j = 0; j < N / 4; ++j) {
+    w[j] = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float c = fminf(fmaxf(r[4 * j + i], -127.0f), 127.0f);
+      w[j] |= (uint32_t)(uint8_t)(int8_t)(int)c << (8 * i);
+    }
+  }
+}
+
 // Quantization: QuantizedInputs::new (tensor.rs:321-339) and the 8-bit
 // Data::quantize (weights.rs:117-136).  A wave covers PER consecutive
 // 256-element chunks of one row (4 elements per lane and chunk, 4 groups per
 // chunk); every chunk's load is issued before the first is used, so a wave
 // keeps PER KB (fp32) in flight.  A group's absmax is a max-reduction over its
-// 16 lanes.  The division is the IEEE one and roundf rounds half away from
-// zero, as f32::round.  x holds DT elements; a non-finite one ORs 1 into
+// 16 lanes; quant_pack rounds the elements (the IEEE quotient by the scale,
+// half away from zero, as f32::round).  x holds DT elements; a non-finite one ORs 1 into
 // *nonfinite (Data::read rejects it for weights, QuantizedInputs::new returns
 // None for inputs).  The host guarantees rows * ceil(chunks / PER) < 2^31.
 template <int DT, int PER>
@@ -330,22 +369,10 @@ __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, in
     m = fmaxf(m, __shfl_xor(m, 2));
     m = fmaxf(m, __shfl_xor(m, 4));
     m = fmaxf(m, __shfl_xor(m, 8));
-    const float scale = (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
-    // round(v / scale) with the IEEE quotient, through a reciprocal: a = v *
-    // rcp(scale) is within 2 ulp of v / scale, so rounding a half away from
-    // zero gives the same integer unless a lies within 2^-15 (>= 4 ulp, as
-    // |a| < 128) of a half-integer; those rare elements divide exactly.
-    const float rs = __builtin_amdgcn_rcpf(scale);
-    uint32_t packed = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float a = v[p][i] * rs;
-      const float fa = fabsf(a);
-      float r = roundf(a);
-      if (!(fabsf(fa - floorf(fa) - 0.5f) > 0x1p-15f)) r = roundf(v[p][i] / scale);
-      r = fminf(fmaxf(r, -127.0f), 127.0f);
-      packed |= (uint32_t)(uint8_t)(int8_t)(int)r << (8 * i);
-    }
+    const float scale = quant_scale(m);
+    uint32_t pk[1];
+    quant_pack<4>(v[p], scale, pk);
+    const uint32_t packed = pk[0];
     if (qvec && k0 + 3 < ldq) {
       // Padding bytes [k, ldq) are written as zero (v = 0 there).
       *reinterpret_cast<uint32_t*>(qr + k0) = packed;
@@ -786,13 +813,67 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       const float bg = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
       const float bu = P.bias2 != nullptr && col < P.n ? P.bias2[col] : 0.0f;
       const ExpTab T = exp_table(lane);
+      float hv[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = mw + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         const float yg = s[0][v] + bg, yu = s[0][16 + v] + bu;
-        const float h = silu_wave(yg, T) * yu;
-        if (row < P.m && col < P.n) P.out[(size_t)row * P.n + col] = h;
+        hv[v] = silu_wave(yg, T) * yu;
+        if (row < P.m && col < P.n) P.out[(size_t)row * P.n + col] = hv[v];
         if ((v & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+      }
+      if (P.hq != nullptr) {  // uniform over the launch
+        // h re-quantized for the down projection (qwen.rs:491, QuantizedInputs::new,
+        // tensor.rs:321-339): the block holds 64 whole groups (rows m0.., columns
+        // n0 .. n0+63, n0 a multiple of 64).  The tile goes through the idle LDS
+        // ring, rows padded to HP floats; then 4 consecutive threads take one
+        // row's group, 16 columns each, and compute exactly what k_quantize does.
+        constexpr int HP = 72;
+        static_assert(BM * HP * 4 <= STAGES * (int)sizeof(Stage), "h tile fits the ring");
+        float* th = reinterpret_cast<float*>(&stg[0]);
+        lds_barrier();  // every wave has drained its ring loads and is done reading the ring
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          th[(WR * wm + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)) * HP + 32 * wn + (lane & 31)] = hv[v];
+        lds_barrier();
+        const int t = threadIdx.x, rl = t >> 2, c0 = 16 * (t & 3);
+        const int row = m0 + rl, cb = n0 + c0;
+        float e[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const v4f f = *reinterpret_cast<const v4f*>(th + rl * HP + c0 + 4 * j);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) e[4 * j + i] = f[i];
+        }
+        if (n0 + kGroup > P.n) {  // the last, partial group (uniform): columns past n count as zero, as in k_quantize
+#pragma unroll
+          for (int i = 0; i < 16; ++i) e[i] = cb + i < P.n ? e[i] : 0.0f;
+        }
+        float mx = 0.0f;
+        bool bad = false;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          bad |= !isfinite(e[i]);
+          mx = fmaxf(mx, fabsf(e[i]));
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 1));  // the group's 4 threads are lanes 4j .. 4j+3
+        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        const float scale = quant_scale(mx);
+        uint32_t w4[4];
+        quant_pack<16>(e, scale, w4);
+        if (row < P.m) {
+          int8_t* qr = P.hq + (size_t)row * P.n + cb;
+          if ((P.n & 15) == 0 && ((uintptr_t)P.hq & 15) == 0) {
+            if (cb < P.n) *reinterpret_cast<uint4*>(qr) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              if (cb + i < P.n) qr[i] = (int8_t)(w4[i >> 2] >> (8 * (i & 3)));
+          }
+          if ((t & 3) == 0) P.hs[(size_t)row * ((P.n + kGroup - 1) / kGroup) + nt] = scale;
+        }
+        const unsigned long long bb = __ballot(bad && row < P.m);
+        if (bb != 0 && lane == __builtin_ffsll((long long)bb) - 1) atomicOr(P.hflag, 1u);
       }
       return;
     }

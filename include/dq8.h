@@ -235,10 +235,17 @@ typedef struct dq8_ffn_weights {
  * up tile of the same outputs side by side, so h is stored once and the gate
  * result is never written and read back.  No reference counterpart of its own:
  * it schedules the crate's two apply calls of the FFN together.  gate and up
- * must have the same shape; h is [m][n] (rows layout). */
+ * must have the same shape; h is [m][n] (rows layout).
+ * h_q/h_scales (both or neither; NULL: h is only stored): h is also quantized
+ * for the down projection (qwen.rs:491, QuantizedInputs::new, tensor.rs:321-339)
+ * into h_q [m][n] and h_scales [m][ceil(n/64)], exactly what dq8_quantize(h)
+ * writes; on the one-launch path the launch itself does it, with no second
+ * pass over h.  A non-finite value in h is reported as by dq8_quantize:
+ * nonfinite == NULL synchronizes and returns DQ8_ERR_NONFINITE (h_q/h_scales
+ * then unspecified; h is written); otherwise 1 is ORed into *nonfinite. */
 dq8_status dq8_ffn_gate_up(dq8_ctx *ctx, const dq8_weights *gate, const dq8_weights *up, const int8_t *q,
                            const float *scales, size_t m, const float *gate_bias, const float *up_bias, float *h,
-                           void *stream);
+                           int8_t *h_q, float *h_scales, uint32_t *nonfinite, void *stream);
 /* One layer's FFN chain on the device (qwen.rs:486-492):
  *   h = gate(x)                          Write            (Linear::apply_shared)
  *   h = silu(h) * up(x)                  SwiGlu           (apply_into_shared)

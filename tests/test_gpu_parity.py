@@ -818,12 +818,15 @@ def test_ffn_chain_matches_the_reference_sequence(ctx, m, hidden, inter, lora):
 
 
 @pytest.mark.parametrize("m,hidden,inter", [(130, 256, 384), (40, 256, 384), (24, 128, 96), (300, 1024, 520),
-                                             (1000, 2048, 2048)])
+                                             (1000, 2048, 2048), (65, 128, 100), (129, 256, 72)])
 def test_ffn_gate_up_equals_write_then_swiglu(ctx, m, hidden, inter):
     # dq8_ffn_gate_up stores what the crate's gate Write and up SwiGlu apply
     # calls store (qwen.rs:489-490): the same bits as two dq8_linear calls and as
     # the oracle, with and without biases; more than 64 rows take the one-launch
-    # pair path, fewer the two launches.
+    # pair path, fewer the two launches.  With quantize=True, h is also
+    # quantized (qwen.rs:491): the same bytes and scales as dq8_quantize(h) and
+    # as the oracle's QuantizedInputs::new(h), for widths that end in a partial
+    # group and widths that are not a multiple of 16 (byte stores).
     rng = np.random.default_rng(m * 7 + inter)
     x = make_x(rng, m, hidden, "outliers")
     gv, gs = dq8o.quantize_weights(make_w(rng, inter, hidden))
@@ -839,7 +842,47 @@ def test_ffn_gate_up_equals_write_then_swiglu(ctx, m, hidden, inter):
         ctx.linear(U, q, s, out=h, bias=db[1], epilogue=dq8.SWIGLU)
         assert bits_equal(got, host(h))
         gate = dq8o.linear(x, gv, gs, bias=biases[0], threads=8)
-        assert bits_equal(got, dq8o.linear(x, uv, us, bias=biases[1], result=gate, epilogue=2, threads=8))
+        want_h = dq8o.linear(x, uv, us, bias=biases[1], result=gate, epilogue=2, threads=8)
+        assert bits_equal(got, want_h)
+        hf, hq, hs = ctx.ffn_gate_up(G, U, q, s, biases=db, quantize=True)
+        assert bits_equal(host(hf), want_h)
+        rq, rs = ctx.quantize(hf)
+        assert np.array_equal(host(hq), host(rq)) and bits_equal(host(hs), host(rs))
+        oq, os_ = dq8o.quantize_inputs(want_h, threads=8)
+        assert np.array_equal(host(hq), oq) and bits_equal(host(hs), os_)
+
+
+@pytest.mark.parametrize("m", [200, 24])
+@pytest.mark.parametrize("given", [False, True])
+def test_ffn_gate_up_quantize_reports_a_non_finite_h(ctx, m, given):
+    # h overflowing to infinity in one column: QuantizedInputs::new(h) is None
+    # (tensor.rs:321-339), reported as dq8_quantize reports it: NonFinite
+    # without a flag, 1 ORed into the flag with one; h itself is still stored.
+    hidden, inter = 256, 384
+    rng = np.random.default_rng(m + given)
+    x = rng.standard_normal((m, hidden)).astype(np.float32)
+    gv, gs = dq8o.quantize_weights((rng.standard_normal((inter, hidden)) * 0.05).astype(np.float32))
+    uv, us = dq8o.quantize_weights((rng.standard_normal((inter, hidden)) * 0.05).astype(np.float32))
+    G, U = ctx.weights_from_quantized(dev(gv), dev(gs)), ctx.weights_from_quantized(dev(uv), dev(us))
+    gb = np.zeros(inter, np.float32)
+    ub = np.zeros(inter, np.float32)
+    gb[300], ub[300] = 1e30, 1e30
+    q, s = ctx.quantize(dev(x))
+    gate = dq8o.linear(x, gv, gs, bias=gb, threads=4)
+    want_h = dq8o.linear(x, uv, us, bias=ub, result=gate, epilogue=2, threads=4)
+    assert np.isinf(want_h[:, 300]).all()
+    h = torch.empty((m, inter), dtype=torch.float32, device="cuda")
+    if given:
+        flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ctx.ffn_gate_up(G, U, q, s, h=h, biases=(dev(gb), dev(ub)), quantize=True, nonfinite=flag)
+        assert int(host(flag)[0]) == 1
+    else:
+        with pytest.raises(dq8.NonFinite):
+            ctx.ffn_gate_up(G, U, q, s, h=h, biases=(dev(gb), dev(ub)), quantize=True)
+    assert bits_equal(host(h), want_h)
+    # a finite h afterwards: the flag is not left set by the earlier call
+    hf, hq, hs = ctx.ffn_gate_up(G, U, q, s, quantize=True)
+    assert np.array_equal(host(hq), dq8o.quantize_inputs(host(hf), threads=4)[0])
 
 
 @pytest.mark.parametrize("kind", ["student", "edge"])
