@@ -551,10 +551,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 #ifndef DQ8_QUANT_PER
 #define DQ8_QUANT_PER 1
 #endif
-// Launches of at most this many blocks (three times as many when they mix
-// long and short K) use a ring of STAGES + 1 groups.
+// Launches of at most DQ8_WIDE_DEEP_BLOCKS blocks (at most three per CU, where
+// the deeper ring's LDS costs no occupancy), and launches of at most
+// DQ8_WIDE_DEEP_MIXED blocks that mix long and short K, use a ring of
+// STAGES + 1 groups.
 #ifndef DQ8_WIDE_DEEP_BLOCKS
-#define DQ8_WIDE_DEEP_BLOCKS 511
+#define DQ8_WIDE_DEEP_BLOCKS 768
+#endif
+#ifndef DQ8_WIDE_DEEP_MIXED
+#define DQ8_WIDE_DEEP_MIXED 1533
 #endif
 
 // ---------------------------------------------------------------------------
@@ -2046,18 +2051,20 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
   if (b.total_waves == 0) return hipSuccess;
   const bool lora = !dots && b.any_lora;
   if (kind == 0) {
-    // total_waves counts blocks for the wide kernel.  Blocks that run alone on
-    // a CU wait on load latency between groups; a ring one group deeper hides
-    // it.  That is the case for launches of fewer than two blocks per CU, and
-    // for the trailing long-K blocks of a launch that mixes long and short K
-    // (a layer's projection set over a few questions' rows: 22-28% faster for
-    // 96-192 rows, 1-3% at 384).  Elsewhere the deeper ring's LDS costs
-    // occupancy (1% on a 2048-row prefill).
+    // total_waves counts blocks for the wide kernel.  Blocks that share a CU
+    // with few others wait on load latency between groups; a ring one group
+    // deeper hides it.  That is the case for launches of at most three blocks
+    // per CU (the 2048-row stack's 512- and 768-block launches: 2.4% off its
+    // step; a ring of STAGES + 2 at two blocks per CU measured slower), and for
+    // the trailing long-K blocks of a launch that mixes long and short K (a
+    // layer's projection set over a few questions' rows: 22-28% faster for
+    // 96-192 rows, 1-3% at 384).  Above three blocks per CU the deeper ring's
+    // 46 KB of LDS costs occupancy (1% on a 2048-row prefill).
     constexpr int threads = 64 * DQ8_WIDE_WM * DQ8_WIDE_WN;
     bool has_long = false, has_short = false;
     for (int i = 0; i < b.count; ++i) (b.p[i].g > 32 ? has_long : has_short) = true;
     const bool deep = b.total_waves <= DQ8_WIDE_DEEP_BLOCKS ||
-                      (has_long && has_short && b.total_waves <= 3 * DQ8_WIDE_DEEP_BLOCKS);
+                      (has_long && has_short && b.total_waves <= DQ8_WIDE_DEEP_MIXED);
 #define DQ8_WIDE(S, D, L)                                                                               \
   k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, S, DQ8_WIDE_XCH, DQ8_WIDE_SWZ, D, L> \
       <<<b.total_waves, threads, 0, s>>>(b)
