@@ -284,36 +284,35 @@ __device__ __forceinline__ float quant_scale(float m) {
   return (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
 }
 // N elements of one group: round(v / scale) half away from zero (f32::round of
-// the IEEE quotient), clamped to [-127, 127], packed 4 bytes to a word.
+// the IEEE quotient), as int8 in [-127, 127], packed 4 bytes to a word.
 // The quotient is taken through rs = rcp(scale) (1 ulp): a = v * rs differs from
 // the IEEE quotient Q by less than 2^-15 (|Q| <= 127, relative error < 2^-22).
-// t = a + copysign(0.5, a) is within 2^-18 of a + sign * 0.5, so when t lies
-// more than 2^-14 from every integer, trunc(t) is round(Q); a lane with an
+// u = a + 128 is within 2^-17 of the exact sum, so when u lies more than 2^-14
+// from every half-integer, rint(u) = round(Q) + 128, an integer in [1, 255]
+// (|a| < 127.0001, no clamp needed), converted and packed by v_cvt_pk_u8_f32;
+// the XOR with 0x80 turns it into the two's complement byte.  A lane with an
 // element closer than that (about 1 in 8000 elements) divides all N exactly.
 template <int N>
 __device__ __forceinline__ void quant_pack(const float (&v)[N], float scale, uint32_t (&w)[N / 4]) {
   const float rs = __builtin_amdgcn_rcpf(scale);
   float r[N];
-  float d = 1.0f;
+  float fm = 0.0f;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const float a = v[i] * rs;
-    const float t = a + copysignf(0.5f, a);
-    r[i] = truncf(t);
-    d = fminf(d, fabsf(t - rintf(t)));
+    const float u = v[i] * rs + 128.0f;
+    r[i] = rintf(u);
+    fm = fmaxf(fm, fabsf(u - r[i]));
   }
-  if (!(d > 0x1p-14f)) {
+  if (!(0.5f - fm > 0x1p-14f)) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) r[i] = roundf(v[i] / scale);
+    for (int i = 0; i < N; ++i) r[i] = fminf(fmaxf(roundf(v[i] / scale), -127.0f), 127.0f) + 128.0f;
   }
 #pragma unroll
   for (int j = 0; j < N / 4; ++j) {
-    w[j] = 0;
+    uint32_t x = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float c = fminf(fmaxf(r[4 * j + i], -127.0f), 127.0f);
-      w[j] |= (uint32_t)(uint8_t)(int8_t)(int)c << (8 * i);
-    }
+    for (int i = 0; i < 4; ++i) x = __builtin_amdgcn_cvt_pk_u8_f32(r[4 * j + i], i, x);
+    w[j] = x ^ 0x80808080u;
   }
 }
 

@@ -1,14 +1,16 @@
 """CPU check of the argument behind the device quantizer's rounding shortcut
-(quant_pack in dq8_kernels.hip): for the group scale s = absmax / 127 and
-|v| <= absmax, a = v * rs with rs any float within 1 ulp of 1 / s, and
-t = a + copysign(0.5, a) in float32, trunc(t) equals round-half-away(v / s)
-(the IEEE quotient, f32::round, tensor.rs:321-339 via weights.rs:117-136)
-whenever t lies more than 2^-14 from every integer.  The values are chosen
-next to the rounding boundaries, where the shortcut could go wrong; the
-device's own results are compared with the oracle in the GPU tests."""
+(quant_pack in dq8_kernels.hip).  For the group scale s = absmax / 127 (IEEE
+quotient) and |v| <= absmax, take a = v * rs with rs any float within 1 ulp
+of 1 / s, and u = a + 128 in float32.  Whenever u lies more than 2^-14 from
+every half-integer, rint(u) - 128 equals round-half-away(v / s) (the IEEE
+quotient, f32::round, tensor.rs:321-339 via weights.rs:117-136), and lies in
+[-127, 127] without a clamp.  The values are chosen next to the rounding
+boundaries, where the shortcut could go wrong; the device's own results are
+compared with the oracle in the GPU tests."""
 import numpy as np
 
 F32 = np.float32
+MARGIN = F32(2.0 ** -14)
 
 
 def round_half_away(q):
@@ -17,16 +19,28 @@ def round_half_away(q):
 
 def cases(rng, n):
     m = (rng.uniform(0.1, 100.0, n) * 2.0 ** rng.integers(-30, 30, n)).astype(F32)
+    tiny = rng.random(n) < 0.05  # groups whose scale is FLT_MIN
+    m = np.where(tiny, (rng.uniform(0.0, 127.0, n) * np.finfo(F32).tiny).astype(F32), m).astype(F32)
     s = np.maximum(m / F32(127.0), np.finfo(F32).tiny).astype(F32)
     k = rng.integers(-127, 127, n)
     base = ((k + 0.5) * s.astype(np.float64)).astype(F32)
     v = (base.view(np.int32) + rng.integers(-40, 41, n).astype(np.int32)).view(F32)
     v = np.clip(v, -m, m).astype(F32)
-    # plus plain values, exact ties and the extremes +-absmax
+    # plus plain values and the extremes +-absmax
     plain = (rng.uniform(-1, 1, n) * m).astype(F32)
     v = np.where(rng.random(n) < 0.2, plain, v)
     v = np.where(rng.random(n) < 0.02, m * np.sign(rng.uniform(-1, 1, n)).astype(F32), v).astype(F32)
     return v, s
+
+
+def shortcut(v, s, du, margin):
+    rs = ((F32(1.0) / s).astype(F32).view(np.int32) + du).view(F32)
+    a = (v * rs).astype(F32)
+    u = (a + F32(128.0)).astype(F32)
+    r = np.rint(u).astype(F32)
+    f = (u - r).astype(F32)
+    fast = (F32(0.5) - np.abs(f)).astype(F32) > margin
+    return fast, r.astype(np.float64) - 128.0
 
 
 def test_shortcut_agrees_with_the_ieee_quotient_next_to_boundaries():
@@ -34,16 +48,12 @@ def test_shortcut_agrees_with_the_ieee_quotient_next_to_boundaries():
     taken = 0
     for _ in range(20):
         v, s = cases(rng, 200_000)
-        want = np.clip(round_half_away((v / s).astype(F32).astype(np.float64)), -127, 127)
-        inv = (F32(1.0) / s).astype(F32)
+        want = round_half_away((v / s).astype(F32).astype(np.float64))
+        assert np.abs(want).max() <= 127
         for du in (-1, 0, 1):  # any reciprocal within 1 ulp
-            rs = (inv.view(np.int32) + du).view(F32)
-            a = (v * rs).astype(F32)
-            t = (a + np.copysign(F32(0.5), a).astype(F32)).astype(F32)
-            d = np.abs(t - np.rint(t)).astype(F32)
-            fast = d > F32(2.0 ** -14)
-            got = np.clip(np.trunc(t.astype(np.float64)), -127, 127)
+            fast, got = shortcut(v, s, du, MARGIN)
             assert np.array_equal(got[fast], want[fast])
+            assert np.abs(got[fast]).max() <= 127
             taken += int(fast.sum())
     assert taken > 0
 
@@ -55,12 +65,8 @@ def test_a_tighter_margin_would_be_wrong():
     bad = 0
     for _ in range(5):
         v, s = cases(rng, 200_000)
-        want = np.clip(round_half_away((v / s).astype(F32).astype(np.float64)), -127, 127)
-        inv = (F32(1.0) / s).astype(F32)
+        want = round_half_away((v / s).astype(F32).astype(np.float64))
         for du in (-1, 1):
-            rs = (inv.view(np.int32) + du).view(F32)
-            a = (v * rs).astype(F32)
-            t = (a + np.copysign(F32(0.5), a).astype(F32)).astype(F32)
-            got = np.clip(np.trunc(t.astype(np.float64)), -127, 127)
-            bad += int((got != want).sum())
+            fast, got = shortcut(v, s, du, F32(0.0))
+            bad += int((got[fast] != want[fast]).sum())
     assert bad > 0
