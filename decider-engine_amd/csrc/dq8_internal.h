@@ -64,6 +64,21 @@ struct Proj {
   int pair;
 };
 
+// Division by a fixed d >= 1 for 0 <= n < 2^31 without a divide (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994,
+// Thm 4.2): with l = ceil(log2 d) and mul = ceil(2^(31+l) / d) < 2^32,
+// floor(n / d) = (n * mul) >> (31 + l), since 0 <= mul*d - 2^(31+l) < d <= 2^l.
+struct Divider {
+  uint32_t mul;
+  int shift;
+  static Divider of(uint32_t d) {
+    int l = 0;
+    while ((1ull << l) < d) ++l;
+    return {(uint32_t)(((1ull << (31 + l)) + d - 1) / d), 31 + l};
+  }
+  __host__ __device__ int div(uint32_t n) const { return (int)(((uint64_t)n * mul) >> shift); }
+};
+
 struct Batch {
   Proj p[kMaxBatch];
   int count;

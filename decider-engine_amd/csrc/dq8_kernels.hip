@@ -278,6 +278,28 @@ __device__ __forceinline__ void decode4(const void* base, size_t i, float (&v)[4
   }
 }
 
+// Lane permutations by DPP (no LDS round trip): quad_perm [1,0,3,2] and
+// [2,3,0,1], and rotations by 4 and 8 lanes within each row of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+// Max over each aligned group of 4 lanes, and of 16 lanes, of non-negative,
+// non-NaN floats (absmax partials that start from 0.0f through fmaxf): their
+// bit patterns order as the values do.
+__device__ __forceinline__ float max_quad(float m) {
+  uint32_t b = __builtin_bit_cast(uint32_t, m);
+  b = max(b, dpp<0xB1>(b));
+  b = max(b, dpp<0x4E>(b));
+  return __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float max_row16(float m) {
+  uint32_t b = __builtin_bit_cast(uint32_t, max_quad(m));
+  b = max(b, dpp<0x124>(b));
+  b = max(b, dpp<0x128>(b));
+  return __builtin_bit_cast(float, b);
+}
+
 // One group's scale from its absmax m (weights.rs:117-136): absmax / 127, at
 // least FLT_MIN, 1 for an all-zero group.
 __device__ __forceinline__ float quant_scale(float m) {
@@ -324,15 +346,17 @@ __device__ __forceinline__ void quant_pack(const float (&v)[N], float scale, uin
 // 16 lanes; quant_pack rounds the elements (the IEEE quotient by the scale,
 // half away from zero, as f32::round).  x holds DT elements; a non-finite one ORs 1 into
 // *nonfinite (Data::read rejects it for weights, QuantizedInputs::new returns
-// None for inputs).  The host guarantees rows * ceil(chunks / PER) < 2^31.
+// None for inputs).  The host guarantees rows * ceil(chunks / PER) < 2^31 and
+// passes wdiv, the divider by the waves per row (wave / wpr without a division).
 template <int DT, int PER>
 __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, int rows, int k, int8_t* __restrict__ q,
-                                                  int ldq, float* __restrict__ scales, int lds, uint32_t* nonfinite) {
+                                                  int ldq, float* __restrict__ scales, int lds, uint32_t* nonfinite,
+                                                  Divider wdiv) {
   const int lane = threadIdx.x & 63;
   const int chunks = (k + 255) >> 8;
   const int wpr = (chunks + PER - 1) / PER;  // waves per row
   const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int row = wave / wpr;
+  const int row = wdiv.div((uint32_t)wave);
   if (row >= rows) return;  // wave-uniform
   const int c0 = (wave - row * wpr) * PER;
   const bool vec = (k & 3) == 0 && ((uintptr_t)x & (DT == kDtypeF32 ? 15 : 7)) == 0;
@@ -363,11 +387,7 @@ __global__ __launch_bounds__(256) void k_quantize(const void* __restrict__ x, in
       bad |= !isfinite(v[p][i]);
       m = fmaxf(m, fabsf(v[p][i]));
     }
-    // max over the 16 lanes of this group (fmaxf of non-negative values is order-free)
-    m = fmaxf(m, __shfl_xor(m, 1));
-    m = fmaxf(m, __shfl_xor(m, 2));
-    m = fmaxf(m, __shfl_xor(m, 4));
-    m = fmaxf(m, __shfl_xor(m, 8));
+    m = max_row16(m);  // over the 16 lanes of this group
     const float scale = quant_scale(m);
     uint32_t pk[1];
     quant_pack<4>(v[p], scale, pk);
@@ -860,8 +880,7 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
           bad |= !isfinite(e[i]);
           mx = fmaxf(mx, fabsf(e[i]));
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 1));  // the group's 4 threads are lanes 4j .. 4j+3
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
+        mx = max_quad(mx);  // the group's 4 threads are lanes 4j .. 4j+3
         const float scale = quant_scale(mx);
         uint32_t w4[4];
         quant_pack<16>(e, scale, w4);
@@ -1979,12 +1998,13 @@ hipError_t launch_quantize_raw(const void* x, int dtype, int rows, int k, int8_t
   if (waves == 0) return hipSuccess;
   if (waves >= (1L << 31) - 4) return hipErrorInvalidValue;
   const int blocks = blocks_for(waves, 4);
+  const Divider wdiv = Divider::of((uint32_t)(((k + 255) / 256 + PER - 1) / PER));
   if (dtype == kDtypeBF16)
-    k_quantize<kDtypeBF16, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
+    k_quantize<kDtypeBF16, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite, wdiv);
   else if (dtype == kDtypeF16)
-    k_quantize<kDtypeF16, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
+    k_quantize<kDtypeF16, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite, wdiv);
   else
-    k_quantize<kDtypeF32, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite);
+    k_quantize<kDtypeF32, PER><<<blocks, 256, 0, s>>>(x, rows, k, q, ldq, scales, lds, nonfinite, wdiv);
   return hipGetLastError();
 }
 

@@ -70,3 +70,20 @@ def test_a_tighter_margin_would_be_wrong():
             fast, got = shortcut(v, s, du, F32(0.0))
             bad += int((got[fast] != want[fast]).sum())
     assert bad > 0
+
+
+def test_multiply_shift_division_is_exact_below_2_31():
+    # The quantizer finds a wave's row as floor(n / d) = (n * mul) >> (31 + l),
+    # l = ceil(log2 d), mul = ceil(2^(31+l) / d) (Granlund and Montgomery 1994,
+    # Thm 4.2).  Checked against integer division for divisors up to 2^24 and
+    # numerators next to multiples of d and at the 2^31 - 1 end.
+    rng = np.random.default_rng(3)
+    ds = np.unique(np.r_[np.arange(1, 300), rng.integers(1, 1 << 24, 2000), 1 << 20, (1 << 20) + 1, (1 << 24) - 1])
+    for d in ds.tolist():
+        l = (d - 1).bit_length()
+        mul = ((1 << (31 + l)) + d - 1) // d
+        assert mul < (1 << 32)
+        qs = rng.integers(0, ((1 << 31) - 1) // d + 1, 200, dtype=np.int64)
+        n = np.unique(np.clip(np.r_[qs * d, qs * d - 1, qs * d + d - 1, (1 << 31) - 1, 0], 0, (1 << 31) - 1))
+        got = [(int(v) * mul) >> (31 + l) for v in n.tolist()]
+        assert got == [int(v) // d for v in n.tolist()]
