@@ -259,8 +259,9 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips) {
   } else {
     p.nseg = dq8::skinny_segments(p.g, few_strips);
     p.waves_n = (p.n + dq8::skinny_cols(p.nseg) - 1) / dq8::skinny_cols(p.nseg);
+    // long K: one 16-row tile of a strip per block (kind 2: two per strip)
     const int per_block = 4 / p.nseg;
-    b.total_waves += (p.waves_n + per_block - 1) / per_block;
+    b.total_waves += (p.waves_n + per_block - 1) / per_block * (p.nseg == 4 && kind == 2 ? 2 : 1);
   }
 }
 

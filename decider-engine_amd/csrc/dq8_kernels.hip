@@ -1090,9 +1090,14 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 //    bytes (two groups; 8 whole cache lines per load): lane l fetches row l/8,
 //    16-byte chunk (l%8) ^ (l/8) and lands at slot l, so the MFMA operand
 //    reads are free of bank conflicts.
-//  * long K (G > 32): a strip's groups are interleaved over NSEG = 2 or 4
-//    waves (wave sidx takes the groups g with g % NSEG == sidx), so a strip
-//    has NSEG rings in flight.  Activation fragments join the register ring;
+//  * long K (G > 32): a strip's groups are interleaved over NSEG = 4 waves
+//    (wave sidx takes the groups g with g % NSEG == sidx), so a strip has
+//    NSEG rings in flight.  A block covers one 16-row tile of its strip (17-32
+//    rows: two blocks per strip, the second weight read mostly from L2), so a
+//    ring step is one activation and one weight fragment and the ring can run
+//    8 steps ahead (the load latency under a full stream is microseconds;
+//    both row tiles in one block held the ring to 6 steps at 210 VGPRs, and
+//    deeper went past 256).  Activation fragments join the register ring;
 //    x scales come through LDS in chunks of 8 steps.  Per step every wave
 //    posts its t's to LDS and, after a barrier, the strip's first wave adds
 //    them in group order: every output is still one left-to-right sum.
@@ -1120,11 +1125,11 @@ __device__ __forceinline__ int x_slot(int r, int gg) {
   return 16 * (r * XP + ((gg >> 2) ^ (r % XP))) + 4 * (gg & 3);
 }
 
-// Direct loads of x chunk c (XP pieces of 4 groups per row, ROWS rows) into
-// dst: this wave's share of the ROWS*XP/64 loads.  Needs 16-byte aligned rows
-// of ldxs % 4 == 0 floats.
+// Direct loads of x chunk c (XP pieces of 4 groups per row, ROWS rows from row
+// r0) into dst: this wave's share of the ROWS*XP/64 loads.  Needs 16-byte
+// aligned rows of ldxs % 4 == 0 floats.
 template <int ROWS, int XP>
-__device__ __forceinline__ void issue_x_chunk(const Proj& P, int c, int wid, uint8_t* dst) {
+__device__ __forceinline__ void issue_x_chunk(const Proj& P, int c, int wid, uint8_t* dst, int r0 = 0) {
   constexpr int LOADS = (ROWS * XP + 63) / 64;
   const int last_piece = (P.g + 3) / 4 - 1;
   int ln;  // lane id, read here so that nothing derived from it stays live
@@ -1136,7 +1141,7 @@ __device__ __forceinline__ void issue_x_chunk(const Proj& P, int c, int wid, uin
       const int e = 64 * i + ln;
       const int r = e / XP, pc = (e % XP) ^ (r % XP);
       const int gp = min(c * XP + pc, last_piece);
-      const uint32_t off = (uint32_t)(min(r, P.m - 1) * P.ldxs + 4 * gp) * 4u;
+      const uint32_t off = (uint32_t)(min(r0 + r, P.m - 1) * P.ldxs + 4 * gp) * 4u;
       dma16s(P.xs, off, dst + i * kFragBytes);
     }
   }
@@ -1147,7 +1152,7 @@ __device__ __forceinline__ void issue_x_chunk(const Proj& P, int c, int wid, uin
 // epilogue.  LoRA products: K=1 MFMA with A lane a = mid of row 4*(a/16) + a%4
 // and B lane l = b of column l%16, the x/w scale convention of the group loop.
 template <int RT, int CT, bool LORA>
-__device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, v4f (&s)[RT * CT]) {
+__device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, v4f (&s)[RT * CT], int r0 = 0) {
   constexpr int E = 4 * RT * CT;
   const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1162,7 +1167,7 @@ __device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, v4
     const float* lbc[CT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt)
-      lm[rt] = P.lmid + (size_t)min(16 * rt + 4 * (lane >> 4) + (lane & 3), P.m - 1) * P.rank;
+      lm[rt] = P.lmid + (size_t)min(r0 + 16 * rt + 4 * (lane >> 4) + (lane & 3), P.m - 1) * P.rank;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) lbc[ct] = P.lb + (size_t)min(c0 + 16 * ct + (lane & 15), P.n - 1) * P.rank;
     if (P.rank <= 16) {
@@ -1218,7 +1223,7 @@ __device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, v4
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int e = 4 * (rt * CT + ct) + v;
-        rows[e] = 16 * rt + 4 * (lane >> 4) + v;
+        rows[e] = r0 + 16 * rt + 4 * (lane >> 4) + v;
         cols[e] = c0 + 16 * ct + (lane & 15);
         y[e] = s[rt * CT + ct][v];
       }
@@ -1229,7 +1234,7 @@ __device__ __forceinline__ void skinny_store(const Proj& P, int c0, int lane, v4
 template <int RT, int CT, bool DOTS>
 __device__ __forceinline__ void skinny_group(const Proj& P, int c0, int lane, bool store, int g, const v4i (&a)[RT],
                                              const v4i (&bw)[CT], const float (&x)[RT], const float (&ws)[CT],
-                                             v4f (&t)[RT * CT]) {
+                                             v4f (&t)[RT * CT], int r0 = 0) {
   const v4i magic = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
   const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -1241,7 +1246,7 @@ __device__ __forceinline__ void skinny_group(const Proj& P, int c0, int lane, bo
         if (store) {
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
-            const int row = 16 * rt + 4 * (lane >> 4) + v;
+            const int row = r0 + 16 * rt + 4 * (lane >> 4) + v;
             const int col = c0 + 16 * ct + (lane & 15);
             if (row < P.m && col < P.n) P.dots[((size_t)row * P.n + col) * P.g + g] = dd[v] - kMagicBits;
           }
@@ -1370,7 +1375,7 @@ __device__ __forceinline__ void skinny_short(const Proj& P, int local, int wid, 
 
 // Long K (G > 32): 4/NSEG strips per block, NSEG waves each, one group per wave and step.
 template <int RT, int CT, int DB, int NSEG, bool DOTS, bool LORA>
-__device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, int lane, uint8_t* lds) {
+__device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, int lane, uint8_t* lds, int r0) {
   constexpr int ROWS = 16 * RT, NT = RT * CT, TPB = 4 / NSEG;
   constexpr int XP = 2 * NSEG;                 // x pieces per row of a chunk of 8 steps (8*NSEG groups)
   constexpr int XBYTES = ROWS * XP * 16;
@@ -1389,7 +1394,7 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
 
   const int8_t* pa[RT];
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) pa[rt] = P.q + (size_t)min(16 * rt + (lane & 15), P.m - 1) * P.ldq + 16 * (lane >> 4);
+  for (int rt = 0; rt < RT; ++rt) pa[rt] = P.q + (size_t)min(r0 + 16 * rt + (lane & 15), P.m - 1) * P.ldq + 16 * (lane >> 4);
   const uint8_t* pb[CT];
   const float* pw[CT];
 #pragma unroll
@@ -1434,7 +1439,7 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
     }
   };
 
-  if constexpr (!DOTS) issue_x_chunk<ROWS, XP>(P, 0, wid, xl);
+  if constexpr (!DOTS) issue_x_chunk<ROWS, XP>(P, 0, wid, xl, r0);
 #pragma unroll
   for (int d = 0; d < DB - 1; ++d) {
     issue(aq[d], bq[d], wq[d], min(d, steps - 1));
@@ -1458,7 +1463,7 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (!DOTS) {
       if (chunk_start && (j >> 3) + 1 < chunks)
-        issue_x_chunk<ROWS, XP>(P, (j >> 3) + 1, wid, xl + (((j >> 3) + 1) & 1) * XBYTES);
+        issue_x_chunk<ROWS, XP>(P, (j >> 3) + 1, wid, xl + (((j >> 3) + 1) & 1) * XBYTES, r0);
     }
     const int nd = (d + DB - 1) % DB;
     issue(aq[nd], bq[nd], wq[nd], min(j + DB - 1, steps - 1));
@@ -1474,7 +1479,7 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
       for (int rt = 0; rt < RT; ++rt) x[rt] = *reinterpret_cast<const float*>(xc + x_slot<XP>(xr[rt], gg));
     }
     v4f t[NT];
-    skinny_group<RT, CT, DOTS>(P, c0, lane, live && g < G, g, aq[d], bq[d], x, wq[d], t);
+    skinny_group<RT, CT, DOTS>(P, c0, lane, live && g < G, g, aq[d], bq[d], x, wq[d], t, r0);
     if constexpr (!DOTS) {
 #pragma unroll
       for (int k = 0; k < NT; ++k) tb[j & 1][wid][k][lane] = t[k];
@@ -1494,7 +1499,7 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
   }
   wait_vmcnt<0>();  // the clamped loads past the end
   if constexpr (!DOTS)
-    if (live && sidx == 0) skinny_store<RT, CT, LORA>(P, c0, lane, s);
+    if (live && sidx == 0) skinny_store<RT, CT, LORA>(P, c0, lane, s, r0);
 }
 
 template <int RT, int CT, int CTL, int DBS, int DBL, bool DOTS, bool LORA>
@@ -1507,8 +1512,8 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   const int local = blockIdx.x - P.wave_begin;
   if (P.nseg == 1)
     skinny_short<RT, CT, DBS, DOTS, LORA>(P, local, wid, lane, lds);
-  else
-    skinny_long<RT, CTL, DBL, 4, DOTS, LORA>(P, local, wid, lane, lds);
+  else  // one 16-row tile per block: 17-32 rows take two blocks per strip
+    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, local / RT, wid, lane, lds, 16 * (local % RT));
 }
 // LoRA middle product (weights.rs:480, 495): mid[r][j] = dot_scores(x_r, a_j)
 // + 0.0 for x [m][k], a [rank][k], in dot_scores' x86-64 order (tensor.rs:6-25).
@@ -2058,6 +2063,9 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
 #endif
 // Short K (G <= 32) runs one wave per strip; longer K interleaves a strip's
 // groups over 4 waves.
+#ifndef DQ8_SKINNY_DBL2
+#define DQ8_SKINNY_DBL2 8  // the long-K ring of the 17-32 row kernel
+#endif
 #ifndef DQ8_SKINNY_SHORT_MAX_G
 #define DQ8_SKINNY_SHORT_MAX_G 32
 #endif
@@ -2096,7 +2104,8 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
   }
   // total_waves counts blocks of 4 waves for the skinny kernel; kind 1: M <= 16, kind 2: M <= 32
   constexpr int CT = DQ8_SKINNY_CT, CL = DQ8_SKINNY_CTL, DS = DQ8_SKINNY_DBS, DL = DQ8_SKINNY_DBL;
-#define DQ8_SKINNY(R, D, L) k_linear_skinny<R, CT, CL, DS, DL, D, L><<<b.total_waves, 256, 0, s>>>(b)
+#define DQ8_SKINNY(R, D, L) \
+  k_linear_skinny<R, CT, CL, DS, (R == 1 ? DL : DQ8_SKINNY_DBL2), D, L><<<b.total_waves, 256, 0, s>>>(b)
   if (kind == 1) {
     if (dots) DQ8_SKINNY(1, true, false);
     else if (lora) DQ8_SKINNY(1, false, true);
