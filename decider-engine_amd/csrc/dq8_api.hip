@@ -818,6 +818,7 @@ dq8_status dq8_quantize(dq8_ctx* ctx, const float* x, size_t m, size_t k, int8_t
   if (m == 0) return DQ8_OK;
   DeviceGuard guard(ctx->device);
   hipStream_t s = (hipStream_t)stream;
+  if (!nonfinite && capturing(s)) return DQ8_ERR_CAPTURE;  // it would synchronize
   uint32_t* flag = nonfinite ? nonfinite : ctx->flag;
   hipError_t e = hipSuccess;
   if (!nonfinite) e = dq8::launch_fill_u32(ctx->flag, 0, s);
@@ -972,6 +973,7 @@ dq8_status dq8_ffn_gate_up(dq8_ctx* ctx, const dq8_weights* gate, const dq8_weig
   DeviceGuard guard(ctx->device);
   hipStream_t s = (hipStream_t)stream;
   if (!h_q) return gate_up(ctx, gate, up, q, scales, m, gate_bias, up_bias, nullptr, nullptr, h, nullptr, s);
+  if (!nonfinite && capturing(s)) return DQ8_ERR_CAPTURE;  // it would synchronize
   if (!nonfinite) {
     hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
     if (e != hipSuccess) return from_hip(e);
@@ -988,6 +990,7 @@ dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, 
   if (st != DQ8_OK || m == 0) return st;
   DeviceGuard guard(ctx->device);
   hipStream_t s = (hipStream_t)stream;
+  if (capturing(s)) return DQ8_ERR_CAPTURE;  // it synchronizes
   WorkInputs in;
   st = quantize_to_work(ctx, w->w, x, m, s, in);
   if (st != DQ8_OK) return st;
@@ -1045,6 +1048,7 @@ dq8_status dq8_linear_q(dq8_ctx* ctx, const dq8_weights* w, const int8_t* q, con
   if (w->w.device != ctx->device) return DQ8_ERR_ARG;
   DeviceGuard guard(ctx->device);
   hipStream_t s = (hipStream_t)stream;
+  if (!nonfinite && capturing(s)) return DQ8_ERR_CAPTURE;  // it would synchronize
   if (!nonfinite) {
     hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
     if (e != hipSuccess) return from_hip(e);

@@ -31,7 +31,9 @@
  *     largest size).  A workspace that is outgrown is kept, not freed, until
  *     dq8_destroy, so graphs captured earlier stay valid.  Calls that
  *     synchronize by design (weight creation and loads, dq8_quantize /
- *     dq8_linear_q with nonfinite == NULL, dq8_linear_f32in) cannot be captured.
+ *     dq8_linear_q / dq8_ffn_gate_up with h_q, each with nonfinite == NULL,
+ *     and dq8_linear_f32in) cannot be captured: on a capturing stream they
+ *     return DQ8_ERR_CAPTURE and enqueue nothing.
  *   - The library starts no threads.
  *   - Weight loads keep their device buffers (stored elements, and values and
  *     scales before the repack) in the context, grown to the largest tensor

@@ -169,3 +169,58 @@ def test_capture_does_not_grow_and_earlier_graphs_survive_growth():
     finally:
         torch.cuda.synchronize()
         c.close()
+
+
+def test_synchronizing_calls_refuse_capture_and_enqueue_nothing(ctx):
+    # Calls that report a non-finite input by synchronizing (no flag pointer
+    # given) return CAPTURE on a capturing stream before enqueuing anything,
+    # so the capture stays usable: the same stream then captures and replays
+    # the flag-pointer forms of the same calls, bit-exact to eager.
+    rng = np.random.default_rng(93)
+    H, F, M = 256, 384, 130
+    mk = lambda n, k: ctx.weights_from_quantized(*(dev(t) for t in dq8o.quantize_weights(
+        (rng.standard_normal((n, k)) * 0.05).astype(np.float32))))
+    wq, wg, wu = mk(H, H), mk(F, H), mk(F, H)
+    x = dev(rng.standard_normal((M, H)).astype(np.float32))
+    q, s = ctx.quantize(x)
+    out = torch.zeros((M, H), dtype=torch.float32, device="cuda")
+    h = torch.zeros((M, F), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.Stream()
+    refusing = [lambda: ctx.quantize(x), lambda: ctx.linear_q(wq, q, s, out=out),
+                lambda: ctx.ffn_gate_up(wg, wu, q, s, h=h, quantize=True), lambda: ctx.linear_f32in(wq, x, out=out)]
+    for call in refusing:
+        g = torch.cuda.CUDAGraph()
+        with pytest.raises(dq8.Dq8Error) as err:
+            with torch.cuda.graph(g, stream=stream):
+                call()
+        assert err.value.status == dq8.ERR_CAPTURE
+    torch.cuda.synchronize()
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    qo = torch.empty((M, H), dtype=torch.int8, device="cuda")
+    so = torch.empty((M, H // 64), dtype=torch.float32, device="cuda")
+    hq = torch.empty((M, F), dtype=torch.int8, device="cuda")
+    hs = torch.empty((M, F // 64), dtype=torch.float32, device="cuda")
+
+    def step():
+        ctx.quantize(x, qo, so, nonfinite=flag)
+        lib = dq8.lib()
+        assert lib.dq8_ffn_gate_up(ctx.handle, wg.handle, wu.handle, qo.data_ptr(), so.data_ptr(), M, None, None,
+                                   h.data_ptr(), hq.data_ptr(), hs.data_ptr(), flag.data_ptr(),
+                                   stream.cuda_stream) == 0
+
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.synchronize()
+    want = [host(t) for t in (qo, so, h, hq, hs)]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        step()
+    for _ in range(3):
+        for t in (qo, so, h, hq, hs):
+            t.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for a, b in zip((qo, so, h, hq, hs), want):
+            assert bits_equal(host(a), b)
+    assert int(host(flag)[0]) == 0
