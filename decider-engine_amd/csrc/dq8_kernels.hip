@@ -1093,8 +1093,9 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 //  * long K (G > 32): a strip's groups are interleaved over NSEG = 4 waves
 //    (wave sidx takes the groups g with g % NSEG == sidx), so a strip has
 //    NSEG rings in flight.  A block covers one 16-row tile of its strip (17-32
-//    rows: two blocks per strip, the second weight read mostly from L2), so a
-//    ring step is one activation and one weight fragment and the ring can run
+//    rows: two blocks per strip, so each weight byte is read twice, the second
+//    time mostly from cache), so a ring step is one activation and one weight
+//    fragment and the ring can run
 //    8 steps ahead (the load latency under a full stream is microseconds;
 //    both row tiles in one block held the ring to 6 steps at 210 VGPRs, and
 //    deeper went past 256).  Activation fragments join the register ring;
@@ -1373,7 +1374,8 @@ __device__ __forceinline__ void skinny_short(const Proj& P, int local, int wid, 
     if (live) skinny_store<RT, CT, LORA>(P, c0, lane, s);
 }
 
-// Long K (G > 32): 4/NSEG strips per block, NSEG waves each, one group per wave and step.
+// Long K (G > 32): one strip per block (TPB = 4/NSEG = 1), its 16*RT rows from row
+// r0, NSEG waves, one group per wave and step.
 template <int RT, int CT, int DB, int NSEG, bool DOTS, bool LORA>
 __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, int lane, uint8_t* lds, int r0) {
   constexpr int ROWS = 16 * RT, NT = RT * CT, TPB = 4 / NSEG;
@@ -2061,11 +2063,11 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
 #ifndef DQ8_SKINNY_DBL
 #define DQ8_SKINNY_DBL 6
 #endif
-// Short K (G <= 32) runs one wave per strip; longer K interleaves a strip's
-// groups over 4 waves.
 #ifndef DQ8_SKINNY_DBL2
 #define DQ8_SKINNY_DBL2 8  // the long-K ring of the 17-32 row kernel
 #endif
+// Short K (G <= 32) runs one wave per strip; longer K interleaves a strip's
+// groups over 4 waves.
 #ifndef DQ8_SKINNY_SHORT_MAX_G
 #define DQ8_SKINNY_SHORT_MAX_G 32
 #endif
