@@ -933,3 +933,43 @@ def test_full_size_gdn_in_projection_properties(ctx):
     h1 = ctx.weights_from_quantized(dev(wv[:cut]), dev(ws[:cut]))
     h2 = ctx.weights_from_quantized(dev(wv[cut:]), dev(ws[cut:]))
     assert bits_equal(np.concatenate([host(ctx.linear(h1, q, s)), host(ctx.linear(h2, q, s))], axis=1), full)
+
+
+def test_ffn_gate_up_quantize_edge_groups(ctx):
+    # The pair launch's quantization of h on edge groups.  Weight rows 0-191 are
+    # zero, so those columns of h come from the biases alone: columns 0-63 give
+    # silu(-1000) * 0 = -0 (an all-zero group, scale 1); 64-127 silu(-80) ~
+    # -1.5e-33 times up biases from 1e-10 to 8e-6 (subnormal h only, scale
+    # FLT_MIN, bytes 0 and -1); 128-191 1e18 * 1e18..2e18 (h near 1e36);
+    # 192-255 ordinary values.  h, its bytes and scales must equal the
+    # oracle's h and QuantizedInputs::new(h).
+    m, hidden, inter = 130, 256, 256
+    rng = np.random.default_rng(4242)
+    x = rng.standard_normal((m, hidden)).astype(np.float32)
+    wg = (rng.standard_normal((inter, hidden)) * 0.01).astype(np.float32)
+    wu = (rng.standard_normal((inter, hidden)) * 0.01).astype(np.float32)
+    wg[:192] = 0.0
+    wu[:192] = 0.0
+    gv, gs = dq8o.quantize_weights(wg)
+    uv, us = dq8o.quantize_weights(wu)
+    i64 = np.arange(64, dtype=np.float64)
+    gb = np.zeros(inter, np.float32)
+    ub = np.zeros(inter, np.float32)
+    gb[:64], gb[64:128], gb[128:192] = -1000.0, -80.0, 1e18
+    ub[64:128] = (1e-10 * 10.0 ** (i64 * 4.9 / 63)).astype(np.float32)
+    ub[128:192] = (1e18 * (1.0 + i64 / 64)).astype(np.float32)
+    G, U = ctx.weights_from_quantized(dev(gv), dev(gs)), ctx.weights_from_quantized(dev(uv), dev(us))
+    q, s = ctx.quantize(dev(x))
+    gate = dq8o.linear(x, gv, gs, bias=gb, threads=8)
+    want_h = dq8o.linear(x, uv, us, bias=ub, result=gate, epilogue=2, threads=8)
+    tiny = np.finfo(np.float32).tiny
+    assert np.all(want_h[:, :64] == 0)
+    assert np.all(np.abs(want_h[:, 64:128]) < tiny) and np.any(np.abs(want_h[:, 64:128]) > tiny / 2)
+    assert np.all(np.abs(want_h[:, 128:192]) > 1e35) and np.all(np.isfinite(want_h))
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    h, hq, hs = ctx.ffn_gate_up(G, U, q, s, biases=(dev(gb), dev(ub)), quantize=True, nonfinite=flag)
+    assert bits_equal(host(h), want_h)
+    oq, os_ = dq8o.quantize_inputs(want_h, threads=8)
+    assert np.array_equal(host(hq), oq) and bits_equal(host(hs), os_)
+    assert np.all(host(hs)[:, 0] == 1.0) and np.all(host(hs)[:, 1] == tiny) and np.any(oq[:, 64:128] != 0)
+    assert int(host(flag)[0]) == 0
