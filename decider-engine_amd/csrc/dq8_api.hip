@@ -242,6 +242,48 @@ int kind_of(const dq8::Weights&, size_t m) { return m > 32 ? 0 : m > 16 ? 2 : 1;
 constexpr long kSkinnyFewStrips = 256;
 long short_strips(const dq8::Weights& w) { return (w.n + dq8::skinny_cols(1) - 1) / dq8::skinny_cols(1); }
 
+// Row chunks for the skinny kernel.  Up to 64 rows (rows layout) always run as
+// chunks of at most 32 rows on the skinny kernel.  65-512 rows do when the
+// call's wide launch would be small: at most kSplitWideBlocks blocks (half a
+// block per CU, so every block would run alone on its CU and wait out each
+// group's dependency chain) and at most kSplitBytes of weights read by all the
+// chunks (the first read comes from HBM, the rest mostly from cache).  Rows are
+// independent, so the results are the same bits either way.  Measured
+// (graph-replayed launches): 128 x 2048 -> 2048 17.5 -> 10.2 us, 128 x 2048 ->
+// 6144 18.1 -> 10.9 us, 128 x 6144 -> 2048 Add 48.0 -> 26.2 us, 512 x 2048 ->
+// 2048 18.3 -> 12.6 us; the split lost for 128 x 2048 -> 8224 (18.7 -> 20.1
+// us: 67 MB re-read over 132 blocks), for 2048 -> 6144 from 192 rows and
+// 6144 -> 2048 from 256 rows.
+constexpr long kSplitWideBlocks = 128;
+constexpr double kSplitBytes = 72e6;
+bool may_split(const dq8::Weights& w, size_t m, int layout) {
+  return kind_of(w, m) == 0 && m <= 512 && layout == DQ8_ROWS;
+}
+long wide_blocks(const dq8::Weights& w, size_t m) {
+  return (long)((m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows()) * (w.np / dq8::wide_block_cols());
+}
+double weight_bytes(const dq8::Weights& w) { return (double)w.n * w.k + 4.0 * w.n * w.g; }
+size_t row_chunks(const dq8::Weights& w, size_t m, int layout, bool small_call) {
+  if (!may_split(w, m, layout) || (m > 64 && !small_call)) return 1;
+  return (m + 31) / 32;
+}
+// Whether a call's 65-512-row items run as skinny row chunks (see row_chunks).
+template <class Item, class W>
+bool small_call(const Item* items, size_t count, W weights_of) {
+  long blocks = 0;
+  double bytes = 0;
+  for (size_t i = 0; i < count; ++i) {
+    const dq8::Weights& w = weights_of(items[i]);
+    const size_t m = items[i].m;
+    if (m == 0 || kind_of(w, m) != 0) continue;
+    const bool can = may_split(w, m, items[i].layout);
+    if (can && m <= 64) continue;  // split whatever the call
+    blocks += wide_blocks(w, m);
+    if (can) bytes += (double)((m + 31) / 32) * weight_bytes(w);
+  }
+  return blocks <= kSplitWideBlocks && bytes <= kSplitBytes;
+}
+
 // Place a filled projection in a launch of the given kernel kind: its first
 // wave/block, column strips, XCD split and the launch's running total.
 void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips) {
@@ -330,14 +372,15 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
     b.count = b.total_waves = b.any_lora = 0;
     b.unless = unless;
   }
+  const bool small = small_call(items, count, [](const dq8_linear_item& it) -> const dq8::Weights& { return it.w->w; });
   // one-wave strips each skinny launch would have (see kSkinnyFewStrips)
   long strips[dq8::kKinds] = {};
   for (size_t i = 0; i < count; ++i) {
     const dq8_linear_item& it = items[i];
     if (it.m == 0) continue;
-    const bool split = kind_of(it.w->w, it.m) == 0 && it.m <= 64 && it.layout == DQ8_ROWS;
-    const int kind = split ? 2 : kind_of(it.w->w, it.m);
-    strips[kind] += (split ? 2 : 1) * short_strips(it.w->w);
+    const size_t nch = row_chunks(it.w->w, it.m, it.layout, small);
+    const int kind = nch > 1 ? 2 : kind_of(it.w->w, it.m);
+    strips[kind] += (long)nch * short_strips(it.w->w);
   }
   size_t offset = 0;
   // Two passes: projections with long K (more than 32 groups) first, so their
@@ -368,15 +411,14 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
       xs = dst;
       offset += xs_pad_bytes(w, it.m);
     }
-    // 33-64 rows in the rows layout run as two row chunks of at most 32 on the
-    // skinny kernel: the weights are read twice (the chunks run side by side,
-    // so mostly once from HBM), which beats a wide launch of half-empty row
-    // tiles whose long-K blocks trail (measured 44 against 52 us for 48 rows of
-    // a layer's projection set).  Rows are independent, so the results are the
-    // same bits.
-    const bool split = kind_of(w, it.m) == 0 && it.m <= 64 && it.layout == DQ8_ROWS;
-    const int kind = split ? 2 : kind_of(w, it.m);
-    const size_t half = split ? (it.m + 1) / 2 : it.m;
+    // Row chunks of at most 32 rows on the skinny kernel (row_chunks): for 33-64
+    // rows the weights are read twice (the chunks run side by side, so mostly
+    // once from HBM), which beats a wide launch of half-empty row tiles whose
+    // long-K blocks trail (measured 44 against 52 us for 48 rows of a layer's
+    // projection set).  Rows are independent, so the results are the same bits.
+    const size_t nch = row_chunks(w, it.m, it.layout, small);
+    const int kind = nch > 1 ? 2 : kind_of(w, it.m);
+    const size_t half = (it.m + nch - 1) / nch;
     for (size_t r0 = 0; r0 < it.m; r0 += half) {
       const size_t rows = std::min(half, it.m - r0);
       dq8::Batch& b = batch[kind];
@@ -527,10 +569,23 @@ dq8_status launch_one(const dq8::Weights& w, const WorkInputs& in, size_t m, con
   b.total_waves = 0;
   b.any_lora = lora != nullptr;
   b.unless = unless;
-  dq8::Proj& p = b.p[0];
-  fill_proj(p, w, in.q, in.ldq, in.xs, in.ldxs, m, bias, out, nullptr, layout, epilogue, lora);
-  const int kind = kind_of(w, m);
-  place_proj(p, kind, b, short_strips(w) < kSkinnyFewStrips);
+  // (row chunks as in run_linear; at most 512 rows make at most 16 chunks)
+  struct One {
+    size_t m;
+    int layout;
+  } one = {m, layout};
+  const size_t nch = row_chunks(w, m, layout, small_call(&one, 1, [&](const One&) -> const dq8::Weights& { return w; }));
+  static_assert(dq8::kMaxBatch >= 16, "512 rows in chunks of 32");
+  const int kind = nch > 1 ? 2 : kind_of(w, m);
+  const size_t half = (m + nch - 1) / nch;
+  b.count = 0;
+  for (size_t r0 = 0; r0 < m; r0 += half) {
+    dq8::Proj& p = b.p[b.count++];
+    fill_proj(p, w, in.q + r0 * in.ldq, in.ldq, in.xs + r0 * in.ldxs, in.ldxs, std::min(half, m - r0), bias,
+              out + r0 * w.n, nullptr, layout, epilogue, lora);
+    if (p.lora) p.lmid += r0 * p.rank;
+    place_proj(p, kind, b, (long)nch * short_strips(w) < kSkinnyFewStrips);
+  }
   return from_hip(dq8::launch_linear(b, kind, false, s));
 }
 

@@ -973,3 +973,53 @@ def test_ffn_gate_up_quantize_edge_groups(ctx):
     assert np.array_equal(host(hq), oq) and bits_equal(host(hs), os_)
     assert np.all(host(hs)[:, 0] == 1.0) and np.all(host(hs)[:, 1] == tiny) and np.any(oq[:, 64:128] != 0)
     assert int(host(flag)[0]) == 0
+
+
+# 65-512 rows whose wide launch would be small run as 32-row chunks on the
+# skinny kernel (dq8_linear and grouped calls through run_linear, dq8_apply
+# through its own launch); shapes on both sides of the rule's limits.
+SMALL_CALLS = [(65, 2048, 300, dq8.WRITE), (96, 6144, 2048, dq8.ADD), (128, 2048, 2048, dq8.SWIGLU),
+               (128, 2048, 8224, dq8.WRITE), (200, 4096, 100, dq8.ADD), (256, 2048, 512, dq8.WRITE),
+               (384, 2048, 2048, dq8.SWIGLU), (512, 2048, 2048, dq8.WRITE), (512, 6144, 1024, dq8.ADD),
+               (513, 2048, 256, dq8.WRITE)]
+
+
+@pytest.mark.parametrize("m,k,n,ep", SMALL_CALLS)
+def test_small_calls_bit_exact(ctx, m, k, n, ep):
+    rng = np.random.default_rng(m * 7 + k + n + ep)
+    x = make_x(rng, m, k, "student")
+    wv, ws = dq8o.quantize_weights(make_w(rng, n, k))
+    bias = rng.standard_normal(n).astype(np.float32)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    base = rng.standard_normal((m, n)).astype(np.float32)
+    got = host(ctx.linear(h, q, s, out=dev(base.copy()), bias=dev(bias), epilogue=ep))
+    want = dq8o.linear(x, wv, ws, bias=bias, result=base, epilogue=ep, threads=8)
+    assert bits_equal(got, want)
+    # the same rows through dq8_apply (fp32 input, quantized inside, its own launch)
+    got_a = host(ctx.apply(h, dev(x), out=dev(base.copy()), bias=dev(bias), epilogue=ep))
+    assert bits_equal(got_a, want)
+
+
+@pytest.mark.parametrize("m", [100, 300])
+def test_small_call_with_adapter_and_group(ctx, m):
+    # An adapter through the chunked path (its middle-product rows follow the
+    # chunks), and a grouped call whose items are all small.
+    rng = np.random.default_rng(m + 5)
+    k, n, rank = 2048, 640, 16
+    x = make_x(rng, m, k, "outliers")
+    wv, ws = dq8o.quantize_weights(make_w(rng, n, k))
+    a = (rng.standard_normal((rank, k)) * 0.05).astype(np.float32)
+    b = (rng.standard_normal((n, rank)) * 0.05).astype(np.float32)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    lora = dq8.Lora(ctx.lora_mid(dev(x), dev(a)), dev(b), 0.5)
+    got = host(ctx.linear_lora(h, q, s, lora, epilogue=dq8.WRITE))
+    assert bits_equal(got, dq8o.linear_lora(x, wv, ws, a, b, 0.5, threads=8))
+    w2v, w2s = dq8o.quantize_weights(make_w(rng, 512, k))
+    h2 = ctx.weights_from_quantized(dev(w2v), dev(w2s))
+    o1 = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    o2 = torch.zeros((m, 512), dtype=torch.float32, device="cuda")
+    ctx.linear_batch([dq8.Item(h, q, s, o1), dq8.Item(h2, q, s, o2)])
+    assert bits_equal(host(o1), dq8o.linear(x, wv, ws, threads=8))
+    assert bits_equal(host(o2), dq8o.linear(x, w2v, w2s, threads=8))
