@@ -244,25 +244,28 @@ long short_strips(const dq8::Weights& w) { return (w.n + dq8::skinny_cols(1) - 1
 
 // Row chunks for the skinny kernel.  Up to 64 rows (rows layout) always run as
 // chunks of at most 32 rows on the skinny kernel.  65-512 rows do when the
-// call's wide launch would be small: at most kSplitWideBlocks blocks (half a
+// call's wide launch would be small: at most kSplitWideBlocks blocks (under one
 // block per CU, so every block would run alone on its CU and wait out each
-// group's dependency chain) and at most kSplitBytes of weights read by all the
-// chunks (the first read comes from HBM, the rest mostly from cache).  Rows are
-// independent, so the results are the same bits either way.  Measured
-// (graph-replayed launches): 128 x 2048 -> 2048 17.5 -> 10.2 us, 128 x 2048 ->
-// 6144 18.1 -> 10.9 us, 128 x 6144 -> 2048 Add 48.0 -> 26.2 us, 512 x 2048 ->
-// 2048 18.3 -> 12.6 us; the split lost for 128 x 2048 -> 8224 (18.7 -> 20.1
-// us: 67 MB re-read over 132 blocks), for 2048 -> 6144 from 192 rows and
-// 6144 -> 2048 from 256 rows.
-constexpr long kSplitWideBlocks = 128;
-constexpr double kSplitBytes = 72e6;
+// group's dependency chain), at most kSplitBytes of weights read by all the
+// chunks (the first read comes from HBM, the rest mostly from cache), and no
+// projection's weights above kSplitWeightBytes (larger ones are re-read from
+// the MALL rather than L2).  Rows are independent, so the results are the same
+// bits either way.  Measured (graph-replayed launches, wide -> chunks):
+// 128 x 2048 -> 2048 17.5 -> 10.2 us, 128 x 2048 -> 6144 18.1 -> 10.9 us,
+// 192 x 2048 -> 6144 18.4 -> 14.7 us, 192 x 6144 -> 2048 Add 48.1 -> 38.1 us,
+// 512 x 2048 -> 2048 18.3 -> 12.6 us.  The chunks lost for 128 x 2048 -> 8224
+// (18.7 -> 20.1 us), 256 x 6144 -> 2048 Add (48.3 -> 50.3 us) and 384 x 2048
+// -> 6144 (23.6 -> 24.1 us).
+constexpr long kSplitWideBlocks = 192;
+constexpr double kSplitBytes = 96e6;
+constexpr double kSplitWeightBytes = 16e6;
+double weight_bytes(const dq8::Weights& w) { return (double)w.n * w.k + 4.0 * w.n * w.g; }
 bool may_split(const dq8::Weights& w, size_t m, int layout) {
-  return kind_of(w, m) == 0 && m <= 512 && layout == DQ8_ROWS;
+  return kind_of(w, m) == 0 && layout == DQ8_ROWS && (m <= 64 || (m <= 512 && weight_bytes(w) <= kSplitWeightBytes));
 }
 long wide_blocks(const dq8::Weights& w, size_t m) {
   return (long)((m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows()) * (w.np / dq8::wide_block_cols());
 }
-double weight_bytes(const dq8::Weights& w) { return (double)w.n * w.k + 4.0 * w.n * w.g; }
 size_t row_chunks(const dq8::Weights& w, size_t m, int layout, bool small_call) {
   if (!may_split(w, m, layout) || (m > 64 && !small_call)) return 1;
   return (m + 31) / 32;

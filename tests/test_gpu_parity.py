@@ -981,7 +981,8 @@ def test_ffn_gate_up_quantize_edge_groups(ctx):
 SMALL_CALLS = [(65, 2048, 300, dq8.WRITE), (96, 6144, 2048, dq8.ADD), (128, 2048, 2048, dq8.SWIGLU),
                (128, 2048, 8224, dq8.WRITE), (200, 4096, 100, dq8.ADD), (256, 2048, 512, dq8.WRITE),
                (384, 2048, 2048, dq8.SWIGLU), (512, 2048, 2048, dq8.WRITE), (512, 6144, 1024, dq8.ADD),
-               (513, 2048, 256, dq8.WRITE)]
+               (513, 2048, 256, dq8.WRITE), (192, 2048, 6144, dq8.SWIGLU), (192, 6144, 2048, dq8.ADD),
+               (256, 6144, 2048, dq8.ADD)]
 
 
 @pytest.mark.parametrize("m,k,n,ep", SMALL_CALLS)
