@@ -20,7 +20,8 @@ by layer with their rows stacked into one 384-row launch per layer set.
 
 "roofline" is for the dominant kernel (the wide projection kernel): achieved
 = algorithmic int8 ops per launch / its average launch time from HIP events on
-the launch stream.
+the launch stream (launches queued behind a GPU lead, so that the events time
+the kernels rather than their submission from the host).
 
 Further legs, each timed on its own: "config1" (one 128 x 2048 -> 2048 linear,
 seed 0), "config2" (the 512-token SwiGLU FFN block through dq8_ffn), "config3"
@@ -75,6 +76,25 @@ def parse():
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run a plain 1 GiB device copy (for rocprof counter calibration)")
     return p.parse_args()
+
+
+_SLEEP_CYCLES_PER_MS = None
+
+
+def gpu_lead(torch, stream, ms):
+    """Queue about ms of GPU work (torch's spin kernel) on the stream ahead of evented launches: the host's
+    submissions then run ahead of the GPU, so each event pair brackets a kernel that was already queued, not
+    the host's submission of it (which shows for kernels of a few tens of microseconds)."""
+    global _SLEEP_CYCLES_PER_MS
+    if _SLEEP_CYCLES_PER_MS is None:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1 << 16)
+        a.record(stream)
+        torch.cuda._sleep(1 << 22)
+        b.record(stream)
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_MS = (1 << 22) / max(a.elapsed_time(b), 1e-3)
+    torch.cuda._sleep(int(ms * _SLEEP_CYCLES_PER_MS))
 
 
 def student_t(torch, gen, shape, device):
@@ -313,6 +333,7 @@ def main():
     ev_steps = args.steps
     ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in calls]
           for _ in range(ev_steps)]
+    gpu_lead(torch, stream, 5.0)
     for s in range(ev_steps):
         run_step(ev[s])
     torch.cuda.synchronize()
@@ -602,10 +623,16 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
     for r in range(reps):
-        go(evs[r])
+        go()
     t1.record(stream)
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
+    # per-launch durations: the same launches again, queued behind a GPU lead so that the events time the
+    # kernels, not the host's submission of each (the eager rate above includes that)
+    gpu_lead(torch, stream, 10.0)
+    for r in range(reps):
+        go(evs[r])
+    torch.cuda.synchronize()
     launch_ms = sum(evs[r][i][0].elapsed_time(evs[r][i][1]) for r in range(reps) for i in range(len(launches)))
     avg_launch = launch_ms / (reps * len(launches))
     # MALL-resident comparison: the same launch (one weight copy) repeated

@@ -156,6 +156,20 @@ __device__ __forceinline__ float silu_wave(float x, const ExpTab& T) {
   return x * rq;
 }
 
+#ifndef DQ8_NT_OUT
+#define DQ8_NT_OUT 1
+#endif
+// One fp32 output store.  Outputs are written once and never re-read by the
+// kernel that writes them, so the stores are marked non-temporal (build with
+// -DDQ8_NT_OUT=0 for plain stores); the bits stored are the same either way.
+__device__ __forceinline__ void st_out(float* p, float v) {
+#if DQ8_NT_OUT
+  __builtin_nontemporal_store(v, p);
+#else
+  *p = v;
+#endif
+}
+
 // Epilogue::store (tensor.rs:92-99) through write_columns (tensor.rs:272-288)
 // for E values of one lane at (row[e], col[e]); elements outside m x n are
 // skipped.  Layout and epilogue are uniform, so they are branched on once, and
@@ -166,13 +180,13 @@ __device__ __forceinline__ void store_tile(const Proj& P, const int (&row)[E], c
   if (P.layout == 1) {
 #pragma unroll
     for (int e = 0; e < E; ++e)
-      if (row[e] < P.m && col[e] < P.n) P.out[(size_t)col[e] * P.m + row[e]] = y[e];
+      if (row[e] < P.m && col[e] < P.n) st_out(P.out + (size_t)col[e] * P.m + row[e], y[e]);
     return;
   }
   if (P.epilogue == 0) {
 #pragma unroll
     for (int e = 0; e < E; ++e)
-      if (row[e] < P.m && col[e] < P.n) P.out[(size_t)row[e] * P.n + col[e]] = y[e];
+      if (row[e] < P.m && col[e] < P.n) st_out(P.out + (size_t)row[e] * P.n + col[e], y[e]);
     return;
   }
   float old[E];
@@ -182,7 +196,7 @@ __device__ __forceinline__ void store_tile(const Proj& P, const int (&row)[E], c
   if (P.epilogue == 1) {
 #pragma unroll
     for (int e = 0; e < E; ++e)
-      if (row[e] < P.m && col[e] < P.n) P.out[(size_t)row[e] * P.n + col[e]] = old[e] + y[e];
+      if (row[e] < P.m && col[e] < P.n) st_out(P.out + (size_t)row[e] * P.n + col[e], old[e] + y[e]);
     return;
   }
   // SwiGlu: each silu with all lanes active, then its store; a few elements
@@ -191,7 +205,7 @@ __device__ __forceinline__ void store_tile(const Proj& P, const int (&row)[E], c
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const float sv = silu_wave(old[e], T);
-    if (row[e] < P.m && col[e] < P.n) P.out[(size_t)row[e] * P.n + col[e]] = sv * y[e];
+    if (row[e] < P.m && col[e] < P.n) st_out(P.out + (size_t)row[e] * P.n + col[e], sv * y[e]);
     if ((e & 3) == 3) __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -540,7 +554,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Launch shape of the wide kernel (tunable at build time): WM x WN waves per
 // block, each wave (32*RT) rows x (32*CT) columns; STAGES groups in flight in
-// LDS; x-scale chunk of XCH groups; A-slab swizzle SWZ (0: for 16-lane LDS
+// LDS where the rings are not split (below); x-scale chunk of XCH groups
+// there; A-slab swizzle SWZ (0: for 16-lane LDS
 // phases, 1: for 8-lane); WPE > 0 caps registers for that many waves per SIMD.
 #ifndef DQ8_WIDE_WM
 #define DQ8_WIDE_WM 2
@@ -573,7 +588,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 // Launches of at most DQ8_WIDE_DEEP_BLOCKS blocks (at most three per CU, where
 // the deeper ring's LDS costs no occupancy), and launches of at most
 // DQ8_WIDE_DEEP_MIXED blocks that mix long and short K, use a ring of
-// STAGES + 1 groups.
+// STAGES + 1 groups.  DQ8_WIDE_SPLIT selects the rings of the other launches:
+// 0: STAGES groups for A and B; 1: split rings, A for 2 groups and B for 3
+// (37.5 KB with 8-group x chunks, so 4 blocks still fit a CU); 2: split rings
+// for every launch.
+#ifndef DQ8_WIDE_SPLIT
+#define DQ8_WIDE_SPLIT 1
+#endif
 #ifndef DQ8_WIDE_DEEP_BLOCKS
 #define DQ8_WIDE_DEEP_BLOCKS 768
 #endif
@@ -610,18 +631,21 @@ __device__ __forceinline__ void wait_vmcnt() {
 // constants; an x-scale chunk is issued just before the group loads of its
 // first group and is therefore complete when that group is.
 //
-// STAGES groups are in flight in an LDS ring.  Iteration g: wait for this
-// wave's loads of group g (vmcnt <= loads of the STAGES-2 newer groups),
-// barrier (every wave's loads of group g have landed and every wave is done
-// reading group g-1), issue the loads of group g+STAGES-1 into group g-1's
-// buffer, then read group g and compute.  Groups past the end load clamped
-// operands and the all-zero w-scale row G; they are never computed on.
+// Two LDS rings: A slabs of SA groups, B fragments and w scales of SB groups
+// (SA == SB, or SA = 2 and SB = 3).  Iteration g: wait for this wave's loads
+// of group g, barrier (every wave's loads of group g have landed and every
+// wave is done reading group g-1), issue A of group g+SA-1 and then B of group
+// g+SB-1 into group g-1's slots, then read group g and compute.  The wait is
+// vmcnt <= the loads issued after group g's: with SA == SB the loads of the
+// SB-2 newer groups; with SA = 2 < SB the B loads of iteration g-1 (issued
+// after A of group g; B of group g is older).  Groups past the end load
+// clamped operands and the all-zero w-scale row G; they are never computed on.
 #if DQ8_WIDE_WPE > 0
 #define DQ8_WIDE_ATTR __attribute__((amdgpu_waves_per_eu(DQ8_WIDE_WPE, DQ8_WIDE_WPE)))
 #else
 #define DQ8_WIDE_ATTR
 #endif
-template <int WM, int WN, int RT, int CT, int STAGES, int XCH, int SWZ, bool DOTS, bool LORA>
+template <int WM, int WN, int RT, int CT, int SA, int SB, int XCH, int SWZ, bool DOTS, bool LORA>
 __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batch b) {
   constexpr int NW = WM * WN, WR = 32 * RT, WC = 32 * CT;
   constexpr int BM = WR * WM, BN = WC * WN;
@@ -629,27 +653,40 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   constexpr int BF = BN / 16;                  // B fragments per group
   constexpr int WSD = DOTS ? 0 : BN / 64;      // w-scale loads per group
   constexpr int L16 = (AS + BF) / NW;          // 16-byte loads per wave per group
-  constexpr int LOADS = L16 + (DOTS ? 0 : 1);  // + one w-scale load (or duplicate)
+  constexpr int KA = AS / NW;                  // ... of them A slabs (slots 0 .. KA-1)
+  constexpr int LB = L16 - KA + (DOTS ? 0 : 1);  // B loads per wave per group, with the w-scale load
   constexpr int PPR = XCH / 4;                 // 16-byte x-scale pieces per row
   constexpr int RPD = 64 / PPR;                // rows per x-scale load
   constexpr int XD = BM / RPD;                 // x-scale loads per chunk
-  constexpr int XPW = XD / NW;                 // ... per wave
+  constexpr int XPW = (XD + NW - 1) / NW;       // ... per wave (waves 0 .. XD-1 when XD < NW)
   constexpr int NP = RT == 2 ? CT : 1;         // tile pairs per wave
-  static_assert((AS + BF) % NW == 0, "16-byte loads must split evenly over the waves");
-  static_assert(WSD <= NW && XD % NW == 0 && XPW >= 1, "scale loads per wave");
-  static_assert(XCH == 16 || XCH == 32, "x-scale chunk");
+  // Loads of this wave that may still be in flight when group g is computed:
+  // with SA == SB the LOADS of each of the SB-2 newer groups; with SA = 2 < SB
+  // the B loads of the last iteration, which were issued after A(g).
+  constexpr int WAITN = SA == SB ? (SB - 2) * (KA + LB) : LB;
+  constexpr int PERIOD = SA == SB ? SA : SA * SB;  // ring slots repeat after PERIOD groups
+  static_assert((AS + BF) % NW == 0 && AS % NW == 0, "16-byte loads must split evenly over the waves");
+  static_assert(WSD <= NW && (XD % NW == 0 || NW % XD == 0), "scale loads per wave");
+  static_assert(XCH == 8 || XCH == 16 || XCH == 32, "x-scale chunk");
   static_assert((RT == 2 && (CT == 1 || CT == 2)) || (RT == 1 && CT == 2), "supported wave tiles");
-  static_assert(STAGES >= 2 && STAGES <= 4 && LOADS * (STAGES - 2) + XPW <= 63, "pipeline depth");
-  struct Stage {
-    uint8_t frag[AS + BF][kFragBytes];  // A slabs, then B fragments
+  static_assert(((SA == SB && SB >= 2 && SB <= 4) || (SA == 2 && SB == 3)) && WAITN + XPW <= 63, "pipeline depth");
+  // The LDS rings: A slabs of SA groups, B fragments and w scales of SB groups.
+  struct AStage {
+    uint8_t frag[AS][kFragBytes];
+  };
+  struct BStage {
+    uint8_t frag[BF][kFragBytes];
     float ws[BN];
+  };
+  struct Ring {
+    AStage a[SA];
+    BStage b[SB];
   };
   struct XChunk {
     uint8_t d[XD][kFragBytes];
   };
-  __shared__ __attribute__((aligned(16))) Stage stg[STAGES];
+  __shared__ __attribute__((aligned(16))) Ring ring;
   __shared__ __attribute__((aligned(16))) XChunk xc[DOTS ? 1 : 2];
-  auto stage = [&](int i) -> Stage& { return stg[i]; };
   if (b.unless && *b.unless) return;  // non-finite inputs: the FP32 kernel runs instead
 
   const int lane = threadIdx.x & 63;
@@ -706,10 +743,16 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   // x-scale pieces: load d = k*NW + wid of a chunk covers rows RPD*d .. RPD*d+RPD-1;
   // lane l fetches row l/PPR, piece (l%PPR) ^ (row%PPR).
 
-  auto issue = [&](Stage& S, int g) {
+  auto issue_a = [&](AStage& S, int g) {
     const int gc = min(g, G - 1);
 #pragma unroll
-    for (int k = 0; k < L16; ++k) dma16s(sbase[k] + (size_t)gc * stride[k], loff[k], &S.frag[k * NW + wid][0]);
+    for (int k = 0; k < KA; ++k) dma16s(sbase[k] + (size_t)gc * stride[k], loff[k], &S.frag[k * NW + wid][0]);
+  };
+  auto issue_b = [&](BStage& S, int g) {
+    const int gc = min(g, G - 1);
+#pragma unroll
+    for (int k = KA; k < L16; ++k)
+      dma16s(sbase[k] + (size_t)gc * stride[k], loff[k], &S.frag[k * NW + wid - AS][0]);
     if constexpr (!DOTS) dma4s(wsbase + (size_t)min(g, G) * P.np, (uint32_t)lane * 4, &S.ws[64 * ww]);
   };
   auto issue_x = [&](int c) {  // once per XCH groups: addresses are recomputed here, not kept live
@@ -721,14 +764,16 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 #pragma unroll
     for (int k = 0; k < XPW; ++k) {
       const int d = k * NW + wid;
-      const int r0 = min(m0 + RPD * d, P.m - 1);
-      const uint32_t row = (uint32_t)((min(m0 + RPD * d + xr, P.m - 1) - r0) * P.ldxs * 4);
-      dma16s(P.xs + (size_t)r0 * P.ldxs, row + off, &xc[c & 1].d[d][0]);
+      if (XD % NW == 0 || d < XD) {  // wave-uniform
+        const int r0 = min(m0 + RPD * d, P.m - 1);
+        const uint32_t row = (uint32_t)((min(m0 + RPD * d + xr, P.m - 1) - r0) * P.ldxs * 4);
+        dma16s(P.xs + (size_t)r0 * P.ldxs, row + off, &xc[c & 1].d[d][0]);
+      }
     }
   };
 
   const int wm = wid / WN, wn = wid - (wid / WN) * WN;
-  const int fbw = AS + 2 * CT * wn;  // first B fragment of this wave
+  const int fbw = 2 * CT * wn;  // first B fragment of this wave
   // A operand: lane reads row R = WR*wm + 32r + lane%32, chunk 2h + lane/32.
   int aoff[RT][2];
 #pragma unroll
@@ -757,33 +802,41 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 #pragma unroll
   for (int j = 0; j < NP; ++j) s[j] = zero32;
 
+  // Prologue: A of groups 0 .. SA-2 and B of groups 0 .. SB-2, each A before
+  // the B of its group (the order the waits count on).
   if constexpr (!DOTS) issue_x(0);
 #pragma unroll
-  for (int i = 0; i < STAGES - 1; ++i) {
-    issue(stage(i), i);
+  for (int i = 0; i < SB - 1; ++i) {
+    if (i < SA - 1) issue_a(ring.a[i], i);
+    issue_b(ring.b[i], i);
     __builtin_amdgcn_sched_barrier(0);
   }
-  for (int g0 = 0; g0 < G; g0 += STAGES) {
+  for (int g0 = 0; g0 < G; g0 += PERIOD) {
 #pragma unroll
-    for (int d = 0; d < STAGES; ++d) {
+    for (int d = 0; d < PERIOD; ++d) {
       const int g = g0 + d;
       if (g >= G) break;  // uniform over the block
-      Stage& cur = stage(d);
-      wait_vmcnt<LOADS * (STAGES - 2)>();
+      const AStage& ca = ring.a[d % SA];
+      const BStage& cur = ring.b[d % SB];
+      wait_vmcnt<WAITN>();
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_sched_barrier(0);
-      const int gn = g + STAGES - 1;
+      // A of group g + SA - 1 and B of group g + SB - 1 go to the slots of
+      // group g - 1, which every wave has finished reading (the barrier).
+      const int ga = g + SA - 1, gb = g + SB - 1;
       if constexpr (!DOTS) {
-        if (gn % XCH == 0 && gn < G) issue_x(gn / XCH);
+        if (ga % XCH == 0 && ga < G) issue_x(ga / XCH);
       }
-      issue(stage((d + STAGES - 1) % STAGES), gn);
+      issue_a(ring.a[(d + SA - 1) % SA], ga);
+      issue_b(ring.b[(d + SB - 1) % SB], gb);
       __builtin_amdgcn_sched_barrier(0);
+      const uint8_t* fa = &ca.frag[0][0];
       const uint8_t* fr = &cur.frag[0][0];
       v4i af[RT][2], bf[CT][2];
 #pragma unroll
       for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) af[r][h] = *reinterpret_cast<const v4i*>(fr + aoff[r][h]);
+        for (int h = 0; h < 2; ++h) af[r][h] = *reinterpret_cast<const v4i*>(fa + aoff[r][h]);
 #pragma unroll
       for (int j = 0; j < CT; ++j)
 #pragma unroll
@@ -843,7 +896,7 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
         const int row = mw + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
         const float yg = s[0][v] + bg, yu = s[0][16 + v] + bu;
         hv[v] = silu_wave(yg, T) * yu;
-        if (row < P.m && col < P.n) P.out[(size_t)row * P.n + col] = hv[v];
+        if (row < P.m && col < P.n) st_out(P.out + (size_t)row * P.n + col, hv[v]);
         if ((v & 3) == 3) __builtin_amdgcn_sched_barrier(0);
       }
       if (P.hq != nullptr) {  // uniform over the launch
@@ -853,8 +906,8 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
         // ring, rows padded to HP floats; then 4 consecutive threads take one
         // row's group, 16 columns each, and compute exactly what k_quantize does.
         constexpr int HP = 72;
-        static_assert(BM * HP * 4 <= STAGES * (int)sizeof(Stage), "h tile fits the ring");
-        float* th = reinterpret_cast<float*>(&stg[0]);
+        static_assert(BM * HP * 4 <= (int)sizeof(Ring), "h tile fits the ring");
+        float* th = reinterpret_cast<float*>(&ring);
         lds_barrier();  // every wave has drained its ring loads and is done reading the ring
 #pragma unroll
         for (int v = 0; v < 16; ++v)
@@ -928,9 +981,9 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       // Operand rows of 16 floats, element i of row r at r*16 + (i ^ ((r >> 2) & 15)):
       // the 32 lanes reading one element of 32 consecutive rows hit 32 banks.
       constexpr int WROWS = 32 * RT, WCOLS = 32 * CT, LWAVE = (WROWS + WCOLS) * 16 * 4;
-      constexpr bool FITS = NW * LWAVE <= STAGES * (int)sizeof(Stage);
+      constexpr bool FITS = NW * LWAVE <= (int)sizeof(Ring);
       const bool staged = FITS && P.rank <= 16;
-      float* lmid = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(&stg[0]) + wid * LWAVE);
+      float* lmid = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(&ring) + wid * LWAVE);
       float* lbw = lmid + WROWS * 16;
       auto sw = [](int r, int i) { return r * 16 + (i ^ ((r >> 2) & 15)); };
       if (staged) {
@@ -2094,13 +2147,21 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
     for (int i = 0; i < b.count; ++i) (b.p[i].g > 32 ? has_long : has_short) = true;
     const bool deep = b.total_waves <= DQ8_WIDE_DEEP_BLOCKS ||
                       (has_long && has_short && b.total_waves <= DQ8_WIDE_DEEP_MIXED);
-#define DQ8_WIDE(S, D, L)                                                                               \
-  k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, S, DQ8_WIDE_XCH, DQ8_WIDE_SWZ, D, L> \
+#define DQ8_WIDE(SA, SB, X, D, L)                                                                \
+  k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, SA, SB, X, DQ8_WIDE_SWZ, D, L> \
       <<<b.total_waves, threads, 0, s>>>(b)
-    constexpr int S0 = DQ8_WIDE_STAGES, S1 = DQ8_WIDE_STAGES + 1;
-    if (dots) DQ8_WIDE(S0, true, false);
-    else if (lora) deep ? DQ8_WIDE(S1, false, true) : DQ8_WIDE(S0, false, true);
-    else deep ? DQ8_WIDE(S1, false, false) : DQ8_WIDE(S0, false, false);
+    constexpr int S0 = DQ8_WIDE_STAGES, S1 = DQ8_WIDE_STAGES + 1, X = DQ8_WIDE_XCH;
+    if (dots) DQ8_WIDE(S0, S0, X, true, false);
+#if DQ8_WIDE_SPLIT == 0
+    else if (lora) deep ? DQ8_WIDE(S1, S1, X, false, true) : DQ8_WIDE(S0, S0, X, false, true);
+    else deep ? DQ8_WIDE(S1, S1, X, false, false) : DQ8_WIDE(S0, S0, X, false, false);
+#elif DQ8_WIDE_SPLIT == 1
+    else if (lora) deep ? DQ8_WIDE(S1, S1, X, false, true) : DQ8_WIDE(2, 3, 8, false, true);
+    else deep ? DQ8_WIDE(S1, S1, X, false, false) : DQ8_WIDE(2, 3, 8, false, false);
+#else
+    else if (lora) DQ8_WIDE(2, 3, 8, false, true);
+    else DQ8_WIDE(2, 3, 8, false, false);
+#endif
 #undef DQ8_WIDE
     return hipGetLastError();
   }
