@@ -360,6 +360,21 @@ def main():
         for _ in range(args.warmup):
             qgraph.replay()
         quant_graph_ms = timed(qgraph.replay)
+    # the same inputs through one of torch's own elementwise kernels that reads each input once and writes a
+    # quarter of its size (the quantizer's traffic, less the scales), replayed the same way: what a launch that
+    # moves these bytes reaches
+    quant_torch_ms = None
+    if graph is not None:
+        qins = [L[key] for L in layers for key in ("x", "mix", "ffn")]
+        sink = torch.empty((M, HIDDEN // 4), dtype=torch.float32, device=dev)
+        tgraph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(tgraph, stream=stream):
+            for x in qins:
+                torch.mul(x[:, ::4], 1.0, out=sink)
+        for _ in range(args.warmup):
+            tgraph.replay()
+        quant_torch_ms = timed(tgraph.replay)
+        quant_torch_bytes = sum(x.numel() * 4 + sink.numel() * 4 for x in qins)
     lin_ops_per_launch = sum(c[3][1] for c in calls if c[0] == "linear") / sum(1 for c in calls if c[0] == "linear")
     lin_avg_ms = lin_ms / lin_n
     achieved = lin_ops_per_launch / (lin_avg_ms * 1e-3) / 1e12
@@ -432,6 +447,8 @@ def main():
             "quantize_timing": "the step's quantize calls replayed alone in a HIP graph" if quant_graph_ms else
                                "HIP events around each eager call",
             "quantize_ms_per_step_events": round(quant_ms / ev_steps, 4),
+            "quantize_torch_same_bytes_gbs": round(quant_torch_bytes / (quant_torch_ms * 1e-3) / 1e9, 1)
+            if quant_torch_ms else None,
             "projection_ms_per_step": round(lin_ms / ev_steps, 4),
         },
         "roofline": {
