@@ -340,7 +340,10 @@ dq8_status check_item_args(const dq8_weights* w, const int8_t* q, const float* s
   if (layout != DQ8_ROWS && layout != DQ8_COLUMNS) return DQ8_ERR_ARG;
   if (epilogue != DQ8_WRITE && epilogue != DQ8_ADD && epilogue != DQ8_SWIGLU) return DQ8_ERR_ARG;
   if (layout == DQ8_COLUMNS && epilogue != DQ8_WRITE) return DQ8_ERR_ARG;
-  if (m > (1u << 30)) return DQ8_ERR_SHAPE;
+  // at most 2^39 outputs per item: a launch's block count (at least 64 x 64
+  // outputs per block, summed over the 16 items a batch holds) then stays
+  // below 2^31
+  if (m > (1u << 30) || m * w->w.n > ((size_t)1 << 39)) return DQ8_ERR_SHAPE;
   return DQ8_OK;
 }
 
@@ -1131,7 +1134,7 @@ dq8_status dq8_ffn(dq8_ctx* ctx, const dq8_ffn_weights* f, const int8_t* q, cons
   if (st != DQ8_OK) return st;
   const size_t rank = f->down_lora_a ? f->down_lora_rank : 0;
   if (f->down_lora_a && (!f->down_lora_b || rank == 0 || rank > (1u << 20))) return DQ8_ERR_ARG;
-  if (m > (1u << 30)) return DQ8_ERR_SHAPE;
+  if (m > (1u << 30) || m * std::max((size_t)u.n, (size_t)d.n) > ((size_t)1 << 39)) return DQ8_ERR_SHAPE;
   DeviceGuard guard(ctx->device);
   hipStream_t s = (hipStream_t)stream;
   // chain workspace: q_h [m][inter], scales_h [m][G] (16-byte aligned), down mid [m][rank]

@@ -13,6 +13,8 @@
  *     (dq8_weights) until dq8_weights_free, and its context workspace.
  *   - Nothing crosses the ABI as an exception: every entry returns dq8_status.
  *     Shape errors return DQ8_ERR_SHAPE where the crate panics (assert_eq!).
+ *     A projection call also returns it for m > 2^30 rows or more than 2^39
+ *     outputs (m * n) in one item, which keeps every launch's grid in range.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
  *     Weight handles are immutable after creation, so calls on different
  *     streams may share them.  One context must not be used by two host

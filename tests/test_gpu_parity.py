@@ -123,6 +123,18 @@ def test_weights_from_f32_bit_exact_and_export(ctx, n, k):
     assert bits_equal(host(scales), want_s)
 
 
+def test_linear_rejects_grids_out_of_range(ctx):
+    # m > 2^30 rows, or more than 2^39 outputs in one item: DQ8_ERR_SHAPE before
+    # anything is read or launched (the pointers are stand-ins never dereferenced)
+    rng = np.random.default_rng(3)
+    h = ctx.weights_from_f32(dev(make_w(rng, 2048, 64)))
+    lib = dq8.lib()
+    fake = 256
+    for m in ((1 << 28) + 1, (1 << 30) + 1):
+        assert lib.dq8_linear(ctx.handle, h.handle, fake, fake, m, None, fake, 0, 0, None) == dq8.ERR_SHAPE
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("n,k", WEIGHT_SHAPES)
 def test_weights_from_quantized_round_trip(ctx, n, k):
     rng = np.random.default_rng(n + 17 * k)
