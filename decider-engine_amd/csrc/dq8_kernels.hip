@@ -1565,10 +1565,22 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const Proj& P = b.p[find_proj(b, blockIdx.x)];
   const int local = blockIdx.x - P.wave_begin;
-  if (P.nseg == 1)
+  if (P.nseg == 1) {
     skinny_short<RT, CT, DBS, DOTS, LORA>(P, local, wid, lane, lds);
-  else  // one 16-row tile per block: 17-32 rows take two blocks per strip
-    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, local / RT, wid, lane, lds, 16 * (local % RT));
+  } else if (RT == 1) {
+    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, local, wid, lane, lds, 0);
+  } else {
+    // One 16-row tile per block: 17-32 rows take two blocks per strip.  The
+    // two blocks of a strip are 8 apart (blocks are dealt to the 8 XCDs in
+    // turn), so both run on one XCD and the second read of the strip's weights
+    // is served by that XCD's L2: in each run of 16 blocks, blocks 0-7 take
+    // the first row tile of 8 strips and blocks 8-15 the second.  A last run
+    // of R < 8 strips pairs blocks R apart.
+    const int run = local >> 4, in = local & 15;
+    const int left = P.waves_n - 8 * run;  // strips from this run on
+    const int r = left >= 8 ? 8 : left;
+    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, 8 * run + in % r, wid, lane, lds, 16 * (in / r));
+  }
 }
 // LoRA middle product (weights.rs:480, 495): mid[r][j] = dot_scores(x_r, a_j)
 // + 0.0 for x [m][k], a [rank][k], in dot_scores' x86-64 order (tensor.rs:6-25).
