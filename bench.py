@@ -620,23 +620,16 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
         launches.append(items)
     sh = stream.cuda_stream
 
-    def go(evs=None, warm_copy=False):
-        for qi, items in enumerate(launches):
-            use = launches[0] if warm_copy else items
-            if evs is not None:
-                evs[qi][0].record(stream)
-            st = lib.dq8_linear_batch(ctx.handle, use, len(shapes), sh)
+    def go(warm_copy=False):
+        for items in launches:
+            st = lib.dq8_linear_batch(ctx.handle, launches[0] if warm_copy else items, len(shapes), sh)
             if st != 0:
                 raise dq8.Dq8Error(st, "dq8_linear_batch")
-            if evs is not None:
-                evs[qi][1].record(stream)
 
     for _ in range(2):
         go()
     torch.cuda.synchronize()
     reps = args.skinny_reps
-    evs = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in launches]
-           for _ in range(reps)]
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
     for r in range(reps):
@@ -644,14 +637,17 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
     t1.record(stream)
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
-    # per-launch durations: the same launches again, queued behind a GPU lead so that the events time the
-    # kernels, not the host's submission of each (the eager rate above includes that)
+    # per-launch duration: the same launches again, queued behind a GPU lead so that they run back to back
+    # (the eager rate above includes the host's submission of each), between one pair of events: every call
+    # is one k_linear_skinny launch, so the region's time over the launch count is the kernel's mean duration.
+    # (An event pair around each launch adds ~2.7 us of event processing to a ~20 us launch.)
     gpu_lead(torch, stream, 10.0)
+    t0.record(stream)
     for r in range(reps):
-        go(evs[r])
+        go()
+    t1.record(stream)
     torch.cuda.synchronize()
-    launch_ms = sum(evs[r][i][0].elapsed_time(evs[r][i][1]) for r in range(reps) for i in range(len(launches)))
-    avg_launch = launch_ms / (reps * len(launches))
+    avg_launch = t0.elapsed_time(t1) / (reps * len(launches))
     # MALL-resident comparison: the same launch (one weight copy) repeated
     t0.record(stream)
     for _ in range(reps):
