@@ -177,11 +177,13 @@ def test_group_dots_extremes(ctx):
 
 # Skinny (M <= 32) cases cover both row-tile counts (M <= 16, M <= 32), short K
 # (G <= 32, odd G, G = 1) and long K (G > 32: 4-way split groups, partial last
-# step, several x-scale chunks, K % 64 != 0).
+# step, several x-scale chunks, K % 64 != 0).  Long K at 17-32 rows pairs a
+# strip's two row-tile blocks 8 apart in runs of 8 strips: 13 and 17 strips
+# (200 and 264 outputs) give whole runs followed by a shorter last run.
 LINEAR_SHAPES = [(1, 1, 1), (1, 64, 4), (4, 64, 4), (5, 128, 6), (9, 192, 31), (24, 2048, 100), (32, 131, 70),
                  (33, 100, 9), (67, 128, 8), (64, 2048, 64), (128, 2048, 130), (200, 65, 17), (7, 6144, 33),
                  (24, 6144, 70), (17, 2371, 50), (32, 4096, 40), (16, 2112, 33), (2, 2113, 17), (48, 2048, 96),
-                 (40, 6144, 50), (63, 131, 33), (34, 4160, 20), (96, 2048, 64)]
+                 (40, 6144, 50), (63, 131, 33), (34, 4160, 20), (96, 2048, 64), (24, 6144, 200), (17, 4096, 264)]
 
 
 @pytest.mark.parametrize("m,k,n", LINEAR_SHAPES)
