@@ -52,7 +52,7 @@ sys.path.insert(0, os.path.join(ROOT, "decider-engine_amd"))
 
 PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0    # MI355X HBM3E, 8 TB/s
-HIDDEN, FFN_DIM, GDN_IN = 2048, 6144, 4 * 2048 + 2 * 16
+HIDDEN, FFN_DIM, GDN_IN, KV_DIM = 2048, 6144, 4 * 2048 + 2 * 16, 4 * 128
 LAYER_KINDS = ["gdn", "gdn", "gdn", "gqa"] * 6
 
 
@@ -153,8 +153,8 @@ def main():
             L["out"] = weights(HIDDEN, HIDDEN)
         else:
             L["q"] = weights(HIDDEN, HIDDEN)
-            L["k"] = weights(512, HIDDEN)
-            L["v"] = weights(512, HIDDEN)
+            L["k"] = weights(KV_DIM, HIDDEN)
+            L["v"] = weights(KV_DIM, HIDDEN)
             L["o"] = weights(HIDDEN, HIDDEN)
         L["gate"] = weights(FFN_DIM, HIDDEN)
         L["up"] = weights(FFN_DIM, HIDDEN)
@@ -594,7 +594,7 @@ def run_skinny_lora(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies
 def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
     """16 questions x M tokens, one grouped launch per question over a layer's projections."""
     M = args.question_tokens
-    shapes = [("q", HIDDEN, HIDDEN), ("k", 512, HIDDEN), ("v", 512, HIDDEN), ("o", HIDDEN, HIDDEN),
+    shapes = [("q", HIDDEN, HIDDEN), ("k", KV_DIM, HIDDEN), ("v", KV_DIM, HIDDEN), ("o", HIDDEN, HIDDEN),
               ("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN), ("gate", FFN_DIM, HIDDEN),
               ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
     wbytes = sum(n * k + 4 * n * ((k + 63) // 64) for _, n, k in shapes)
@@ -749,7 +749,7 @@ def run_load(args, torch, dq8, ctx, gen):
     import struct as _struct
     import tempfile
 
-    shapes = [("q", HIDDEN, HIDDEN), ("k", 512, HIDDEN), ("v", 512, HIDDEN), ("o", HIDDEN, HIDDEN),
+    shapes = [("q", HIDDEN, HIDDEN), ("k", KV_DIM, HIDDEN), ("v", KV_DIM, HIDDEN), ("o", HIDDEN, HIDDEN),
               ("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN), ("gate", FFN_DIM, HIDDEN),
               ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
     header, blobs, off = {}, [], 0
@@ -1130,7 +1130,7 @@ def run_host_round_trip(args, torch, dq8, ctx, lib, dev, stream):
                          "device_ms": round(timed_calls(torch, stream, proj, 50), 5),
                          "h2d_bytes": M * HIDDEN * 4, "d2h_bytes": M * HIDDEN * 4}
     w.free()
-    shapes = [("q", HIDDEN, HIDDEN), ("k", 512, HIDDEN), ("v", 512, HIDDEN), ("o", HIDDEN, HIDDEN),
+    shapes = [("q", HIDDEN, HIDDEN), ("k", KV_DIM, HIDDEN), ("v", KV_DIM, HIDDEN), ("o", HIDDEN, HIDDEN),
               ("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN), ("gate", FFN_DIM, HIDDEN),
               ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
     src = {"q": 0, "k": 0, "v": 0, "gdn_in": 0, "gate": 0, "up": 0, "o": 1, "gdn_out": 1, "down": 2}
@@ -1219,9 +1219,9 @@ def run_checks(dq8o, checks, threads):
 def run_cpu_baseline(args, torch, dq8, ctx, dev, gen, checks):
     """The oracle (C restatement of the reference's x86 int8 path: per-projection input quantization +
     per-column scalar group dots, threads over output columns as rayon does, tensor.rs:442-448) on a sample of
-    the stack's workload: one GDN layer's projections + its FFN for a bounded number of token rows.  One
-    warm-up, then the median of 5 timed runs, with all usable host cores and with one.  Then the sampled oracle
-    checks of the timed GPU workloads."""
+    the stack's workload: one period of its 3:1 layer order (three GDN layers and one GQA layer, each with its
+    FFN) for a bounded number of token rows.  One warm-up, then the median of 5 timed runs, with all usable host
+    cores and with one.  Then the sampled oracle checks of the timed GPU workloads."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
@@ -1234,33 +1234,39 @@ def run_cpu_baseline(args, torch, dq8, ctx, dev, gen, checks):
     # at most 16 threads: one GPU's share of the host
     threads = max(1, min(16, nproc, int(os.environ.get("OMP_NUM_THREADS", "16") or 16)))
     rng = np.random.default_rng(5)
-    shapes = [("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN), ("gate", FFN_DIM, HIDDEN),
-              ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
+    gdn = [("gdn_in", GDN_IN, HIDDEN), ("gdn_out", HIDDEN, HIDDEN)]
+    gqa = [("q", HIDDEN, HIDDEN), ("k", KV_DIM, HIDDEN), ("v", KV_DIM, HIDDEN), ("o", HIDDEN, HIDDEN)]
+    ffn = [("gate", FFN_DIM, HIDDEN), ("up", FFN_DIM, HIDDEN), ("down", HIDDEN, FFN_DIM)]
     ws = {}
-    for name, n, k in shapes:
+    for name, n, k in gdn + gqa + ffn:
         h = ctx.weights_from_f32((torch.randn((n, k), generator=gen, device=dev) * 0.02).contiguous())
         ws[name] = exported(torch, h)
         h.free()
 
-    def layer(x, t):
+    def block(x, t):
+        # three GDN layers, then a GQA layer (the stack's 3:1 order), each followed by its FFN; every
+        # projection quantizes its own input, as the crate's linear does
         s = time.perf_counter()
-        dq8o.linear(x, *ws["gdn_in"], threads=t)
-        dq8o.linear(x, *ws["gdn_out"], threads=t)
-        g = dq8o.linear(x, *ws["gate"], threads=t)
-        g = dq8o.linear(x, *ws["up"], result=g, epilogue=2, threads=t)
-        dq8o.linear(g, *ws["down"], result=x, epilogue=1, threads=t)
+        for mixer in ("gdn", "gdn", "gdn", "gqa"):
+            names = ("gdn_in", "gdn_out") if mixer == "gdn" else ("q", "k", "v", "o")
+            for name in names:
+                dq8o.linear(x, *ws[name], threads=t)
+            g = dq8o.linear(x, *ws["gate"], threads=t)
+            g = dq8o.linear(x, *ws["up"], result=g, epilogue=2, threads=t)
+            dq8o.linear(g, *ws["down"], result=x, epilogue=1, threads=t)
         return time.perf_counter() - s
 
-    ops_per_row = 2 * sum(n * k for _, n, k in shapes)
+    ops_per_row = 2 * (3 * sum(n * k for _, n, k in gdn) + sum(n * k for _, n, k in gqa) +
+                       4 * sum(n * k for _, n, k in ffn))
     # size the sample so that one single-thread run takes about cpu_seconds / 10
     probe = rng.standard_normal((4, HIDDEN)).astype(np.float32)
-    per_row = layer(probe, 1) / 4
+    per_row = block(probe, 1) / 4
     rows = int(max(8, min(512, args.cpu_seconds / 10 / per_row)))
     x = rng.standard_normal((rows, HIDDEN)).astype(np.float32)
 
     def median_tops(t):
-        layer(x, t)
-        secs = sorted(layer(x, t) for _ in range(5))[2]
+        block(x, t)
+        secs = sorted(block(x, t) for _ in range(5))[2]
         return ops_per_row * rows / secs / 1e12, secs
 
     tops, secs = median_tops(threads)
@@ -1280,8 +1286,9 @@ def run_cpu_baseline(args, torch, dq8, ctx, dev, gen, checks):
         "unit": "TOPS",
         "cores": threads,
         "kind": "port",
-        "sample": f"GDN layer + FFN projections (in 2048->8224, out, gate/up SwiGlu, re-quantized down) for {rows} "
-                  f"of the stack's 2048 tokens, quantization included; median of 5 runs after 1 warm-up "
+        "sample": f"one period of the stack's 3:1 layer order (3 GDN layers: in 2048->8224, out; 1 GQA layer: q, k, "
+                  f"v, o; each with its FFN: gate/up SwiGlu, re-quantized down) for {rows} of the stack's 2048 "
+                  f"tokens, quantization included; median of 5 runs after 1 warm-up "
                   f"({secs:.2f} s each at {threads} threads, {secs1:.2f} s at 1) on {cpu_model}",
         "value_1_thread": round(tops1, 5),
         "nproc": nproc,
