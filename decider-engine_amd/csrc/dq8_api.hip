@@ -241,6 +241,24 @@ int kind_of(const dq8::Weights&, size_t m) { return m > 32 ? 0 : m > 16 ? 2 : 1;
 // one-wave strips are faster (10.2 against 10.9 us; 30.5 against 40.1 us).
 constexpr long kSkinnyFewStrips = 256;
 long short_strips(const dq8::Weights& w) { return (w.n + dq8::skinny_cols(1) - 1) / dq8::skinny_cols(1); }
+// 16-column units of a short-K projection (one-wave strips hold two).
+long short_units(const dq8::Weights& w) { return w.g <= 32 ? (w.n + 15) / 16 : 0; }
+// Units per block of a skinny launch's short-K projections (8: whole
+// 32-column strips, 4 per block).  Without long-K projections in the launch,
+// the units spread over about one block per CU, at most 7 per block:
+// each CU streams its bytes at a limited rate, so the CU holding the most
+// bytes sets the launch's time (24 rows, graph-replayed: GDN in alone 10.4 ->
+// 8.3 us, gate+up 11.0 -> 8.8 us against 8-unit blocks on fewer CUs).  Two
+// units (one strip) per block at least.  With long-K projections their blocks
+// (one per CU) are the launch's critical path, and short-K blocks on more of
+// their CUs slow them: a layer set with down took 21.1-21.6 us at 8 units per
+// block and 21.5-22.0 us spread out, so such launches keep 8.
+#ifndef DQ8_SKINNY_UNITS_MAX
+#define DQ8_SKINNY_UNITS_MAX 7
+#endif
+int units_per_block(long units, bool has_long) {
+  return has_long ? 8 : (int)std::min((long)DQ8_SKINNY_UNITS_MAX, std::max(2L, (units + 255) / 256));
+}
 
 // Row chunks for the skinny kernel.  Up to 64 rows (rows layout) always run as
 // chunks of at most 32 rows on the skinny kernel.  65-512 rows do when the
@@ -289,7 +307,7 @@ bool small_call(const Item* items, size_t count, W weights_of) {
 
 // Place a filled projection in a launch of the given kernel kind: its first
 // wave/block, column strips, XCD split and the launch's running total.
-void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips) {
+void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips, long launch_units, bool launch_has_long) {
   p.wave_begin = b.total_waves;
   p.xcd_gm = 0;
   p.nseg = 1;
@@ -303,10 +321,16 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips) {
     b.total_waves += p.waves_n * row_tiles;
   } else {
     p.nseg = dq8::skinny_segments(p.g, few_strips);
-    p.waves_n = (p.n + dq8::skinny_cols(p.nseg) - 1) / dq8::skinny_cols(p.nseg);
-    // long K: one 16-row tile of a strip per block (kind 2: two per strip)
-    const int per_block = 4 / p.nseg;
-    b.total_waves += (p.waves_n + per_block - 1) / per_block * (p.nseg == 4 && kind == 2 ? 2 : 1);
+    if (p.nseg == 1) {
+      // short K: 16-column units dealt to blocks, units_per_block at a time
+      p.waves_n = (p.n + 15) / 16;
+      p.units = units_per_block(launch_units, launch_has_long);
+      b.total_waves += (p.waves_n + p.units - 1) / p.units;
+    } else {
+      // long K: one 16-row tile of a strip per block (kind 2: two per strip)
+      p.waves_n = (p.n + dq8::skinny_cols(p.nseg) - 1) / dq8::skinny_cols(p.nseg);
+      b.total_waves += p.waves_n * (kind == 2 ? 2 : 1);
+    }
   }
 }
 
@@ -380,13 +404,16 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
   }
   const bool small = small_call(items, count, [](const dq8_linear_item& it) -> const dq8::Weights& { return it.w->w; });
   // one-wave strips each skinny launch would have (see kSkinnyFewStrips)
-  long strips[dq8::kKinds] = {};
+  long strips[dq8::kKinds] = {}, units[dq8::kKinds] = {};
+  bool has_long[dq8::kKinds] = {};
   for (size_t i = 0; i < count; ++i) {
     const dq8_linear_item& it = items[i];
     if (it.m == 0) continue;
     const size_t nch = row_chunks(it.w->w, it.m, it.layout, small);
     const int kind = nch > 1 ? 2 : kind_of(it.w->w, it.m);
     strips[kind] += (long)nch * short_strips(it.w->w);
+    units[kind] += (long)nch * short_units(it.w->w);
+    has_long[kind] = has_long[kind] || it.w->w.g > 32;
   }
   size_t offset = 0;
   // Two passes: projections with long K (more than 32 groups) first, so their
@@ -444,7 +471,7 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
         p.lmid += r0 * p.rank;
         b.any_lora = 1;
       }
-      place_proj(p, kind, b, strips[kind] < kSkinnyFewStrips);
+      place_proj(p, kind, b, strips[kind] < kSkinnyFewStrips, units[kind], has_long[kind]);
     }
   }
   for (int kind = 0; kind < dq8::kKinds; ++kind) {
@@ -488,7 +515,7 @@ dq8_status run_pair(dq8_ctx* ctx, const dq8::Weights& g, const dq8::Weights& u, 
     p.hflag = qout->nonfinite;
   }
   p.pair = 1;
-  place_proj(p, 0, b, false);
+  place_proj(p, 0, b, false, 0, false);
   return from_hip(dq8::launch_linear(b, 0, false, s));
 }
 
@@ -590,7 +617,7 @@ dq8_status launch_one(const dq8::Weights& w, const WorkInputs& in, size_t m, con
     fill_proj(p, w, in.q + r0 * in.ldq, in.ldq, in.xs + r0 * in.ldxs, in.ldxs, std::min(half, m - r0), bias,
               out + r0 * w.n, nullptr, layout, epilogue, lora);
     if (p.lora) p.lmid += r0 * p.rank;
-    place_proj(p, kind, b, (long)nch * short_strips(w) < kSkinnyFewStrips);
+    place_proj(p, kind, b, (long)nch * short_strips(w) < kSkinnyFewStrips, (long)nch * short_units(w), w.g > 32);
   }
   return from_hip(dq8::launch_linear(b, kind, false, s));
 }

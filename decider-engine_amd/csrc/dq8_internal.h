@@ -46,7 +46,9 @@ struct Proj {
   int epilogue;       // 0 write, 1 add, 2 swiglu
   int layout;         // 0 rows [M][N], 1 columns [N][M]
   int wave_begin;     // first block of this projection in the launch
-  int waves_n;        // column strips (skinny: skinny_cols(nseg) wide, wide: one block tile wide)
+  int waves_n;        // column strips (wide: one block tile wide; skinny long K: 16 columns wide;
+                      // skinny short K: 16-column units, dealt to blocks `units` at a time)
+  int units;          // skinny short K: at most this many 16-column units per block (2..8)
   int xcd_gm;         // wide: row bands of the per-XCD tile regions (1, 2, 4, 8), 0 = row-major order
   int xcd_sr, xcd_sc; // wide: a region is walked in chunks of xcd_sr row tiles x xcd_sc column tiles
   int nseg;           // skinny: waves per strip (1 or 4)

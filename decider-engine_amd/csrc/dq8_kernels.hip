@@ -1313,17 +1313,16 @@ __device__ __forceinline__ void skinny_group(const Proj& P, int c0, int lane, bo
     }
 }
 
-// Short K (G <= 32): 4 strips per block, one wave each, 2 groups per step.
+// Short K (G <= 32): one wave streams the 16*CT columns from c0 over all
+// groups, 2 groups per step.  The block's 4 waves first load its activation
+// together; a wave with no columns (live false) only helps with that.
 template <int RT, int CT, int DB, bool DOTS, bool LORA>
-__device__ __forceinline__ void skinny_short(const Proj& P, int local, int wid, int lane, uint8_t* lds) {
+__device__ __forceinline__ void skinny_short(const Proj& P, int c0, bool live, int wid, int lane, uint8_t* lds) {
   constexpr int ROWS = 16 * RT;
   constexpr int STEP_A = RT * 2 * kFragBytes;  // activation bytes of one step (8-row units)
   constexpr int OPS = 2 * CT * (DOTS ? 1 : 2);  // ring loads per step
   static_assert(DB >= 2 && (DB - 1) * OPS <= 63, "ring depth");
   uint8_t* xl = lds + 16 * STEP_A;  // x scales: one chunk of 32 groups (8 pieces per row)
-  const int strip = local * 4 + wid;
-  const bool live = strip < P.waves_n;  // the last block of a projection may hold fewer strips
-  const int c0 = (live ? strip : 0) * 16 * CT;
   const int G = P.g;
   const int steps = (G + 1) >> 1;
 
@@ -1349,10 +1348,12 @@ __device__ __forceinline__ void skinny_short(const Proj& P, int local, int wid, 
       }
     }
   };
+  if (live) {
 #pragma unroll
-  for (int d = 0; d < DB - 1; ++d) {
-    issue(bq[d], wq[d], min(d, steps - 1));
-    __builtin_amdgcn_sched_barrier(0);
+    for (int d = 0; d < DB - 1; ++d) {
+      issue(bq[d], wq[d], min(d, steps - 1));
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   // Preload: activation unit u = 2*RT*j + o (step j, row octet o), then the x chunk.
   {
@@ -1368,6 +1369,7 @@ __device__ __forceinline__ void skinny_short(const Proj& P, int local, int wid, 
   }
   wait_vmcnt<0>();
   lds_barrier();
+  if (!live) return;  // no later barrier in this path
 
   int aoff[RT][2];  // [row tile][group parity]: row 16rt + l%16, chunk 4*parity + l/16
 #pragma unroll
@@ -1566,7 +1568,28 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   const Proj& P = b.p[find_proj(b, blockIdx.x)];
   const int local = blockIdx.x - P.wave_begin;
   if (P.nseg == 1) {
-    skinny_short<RT, CT, DBS, DOTS, LORA>(P, local, wid, lane, lds);
+    static_assert(CT == 2, "short-K waves take at most two 16-column units");
+    const int H = P.waves_n;  // units of 16 columns
+    int u0, cnt;
+    if (P.units == 8) {
+      // 4 strips of two units per block, one per wave, from unit 8*local
+      u0 = 2 * (4 * local + wid);
+      cnt = u0 < H ? 2 : 0;
+    } else {
+      // The units are dealt to B = ceil(H / units) blocks, floor(b*H/B) ..
+      // floor((b+1)*H/B) to block b (at most 7), so blocks carry equal byte
+      // counts to within one unit, and a block's c units to its waves as
+      // evenly as they go (w*c/4 .. (w+1)*c/4): as many waves stream as the
+      // block has units, up to 4, and none takes more than two.
+      const long B = (H + P.units - 1) / P.units;
+      const int h0 = (int)((long)local * H / B), c = (int)((long)(local + 1) * H / B) - h0;
+      u0 = h0 + wid * c / 4;
+      cnt = h0 + (wid + 1) * c / 4 - u0;
+    }
+    if (cnt == 2)
+      skinny_short<RT, 2, DBS, DOTS, LORA>(P, 16 * u0, true, wid, lane, lds);
+    else
+      skinny_short<RT, 1, DBS, DOTS, LORA>(P, 16 * u0, cnt == 1, wid, lane, lds);
   } else if (RT == 1) {
     skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, local, wid, lane, lds, 0);
   } else {
