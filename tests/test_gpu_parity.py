@@ -388,6 +388,28 @@ def test_linear_batch_full_layer_set(ctx, m):
         assert bits_equal(host(outs[name]), want), name
 
 
+@pytest.mark.parametrize("m", [24, 9, 32])
+def test_linear_batch_short_k_units_dealt(ctx, m):
+    # The layer set's eight short-K projections in one grouped launch, no long-K
+    # item: 1730 units of 16 columns dealt 6 or 7 to a block and one or two to a
+    # wave, so 16- and 32-column pieces start at even and odd units.
+    rng = np.random.default_rng(m + 2000)
+    short = [(name, n, k) for name, n, k in FULL_LAYER if k == 2048]
+    x = make_x(rng, m, 2048, kind="student")
+    q, s = ctx.quantize(dev(x))
+    items, want = [], {}
+    for name, n, k in short:
+        wv, ws = dq8o.quantize_weights(make_w(rng, n, k))
+        bias = rng.standard_normal(n).astype(np.float32) if name in ("o", "gdn_in") else None
+        out = dev(np.zeros((m, n), np.float32))
+        items.append(dq8.Item(ctx.weights_from_quantized(dev(wv), dev(ws)), q, s, out,
+                              bias=None if bias is None else dev(bias)))
+        want[name] = (out, dq8o.linear(x, wv, ws, bias=bias, threads=8))
+    ctx.linear_batch(items)
+    for name, (out, w) in want.items():
+        assert bits_equal(host(out), w), name
+
+
 def test_skinny_short_path_single_projection_with_lora(ctx):
     # 8224 outputs = 257 one-wave strips: a single projection on the short-K path,
     # with a rank-16 adapter
