@@ -661,6 +661,36 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
     # questions); the eager rate above is reported beside it
     lora = run_skinny_lora(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, acts, launches)
     graph_q_ms = lora["plain_ms_per_question"]
+    # the same projections as a model issues them, one launch per input: x (q, k, v, GDN in), the mixer outputs
+    # (o, GDN out), the FFN input (gate, up), h (down); graph-replayed like the grouped launch
+    parts = [[0, 1, 2, 4], [3, 5], [6, 7], [8]]
+    split = []
+    for items in launches:
+        for idx in parts:
+            sub = (dq8._Item * len(idx))()
+            for j, i in enumerate(idx):
+                sub[j] = items[i]
+            split.append(sub)
+
+    def go_split():
+        for sub in split:
+            st = lib.dq8_linear_batch(ctx.handle, sub, len(sub), sh)
+            if st != 0:
+                raise dq8.Dq8Error(st, "dq8_linear_batch")
+
+    go_split()
+    torch.cuda.synchronize()
+    sg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(sg, stream=stream):
+        go_split()
+    sg.replay()
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(reps):
+        sg.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    split_q_ms = t0.elapsed_time(t1) / (reps * args.questions)
     stacked = run_stacked(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, wbytes, graph_q_ms)
     for ws in copies:
         for h in ws:
@@ -686,6 +716,12 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
             "traffic": load_traffic("linear_skinny_questions24"),
             "bytes_per_launch": wbytes,
             "avg_launch_ms": round(avg_launch, 5),
+        },
+        "layer_order_launches": {
+            "workload": "the same questions, each as 4 launches in a layer's order: q,k,v + GDN in (x), o + GDN out "
+                        "(mixer outputs), gate + up (FFN input), down (h); HIP graph replay",
+            "ms_per_question": round(split_q_ms, 5),
+            "gbs": round(wbytes / (split_q_ms * 1e-3) / 1e9, 1),
         },
         "lora": lora,
     }
