@@ -233,13 +233,14 @@ void xcd_chunks(dq8::Proj& p, int row_tiles) {
 // Kernel kind of a projection (see launch_linear).
 int kind_of(const dq8::Weights&, size_t m) { return m > 32 ? 0 : m > 16 ? 2 : 1; }
 
-// A skinny launch whose projections would run on fewer one-wave strips than
+// A skinny launch whose projections would run on fewer 32-column strips than
 // this takes the 4-wave path for all of them: each wave then streams a quarter
 // of a strip's groups, so 4x the waves keep weight loads in flight.  Measured
-// at 24 rows: 2048x2048 9.8 -> 5.7 us, 2048x6144 9.9 -> 8.3 us; at 257 strips
-// (8224 outputs) and in a layer set's grouped launch (~930 strips) the
-// one-wave strips are faster (10.2 against 10.9 us; 30.5 against 40.1 us).
-constexpr long kSkinnyFewStrips = 256;
+// at 24 rows, graph-replayed, 4-wave path against short-K blocks of dealt
+// units: 2048x2048 (64 strips) 4.9 against 8.0 us, o + GDN out (128) 7.6
+// against 8.3 us, 2048x6144 (192) 10.6 against 8.3 us, GDN in (257) 10.4
+// against 8.2 us.
+constexpr long kSkinnyFewStrips = 160;
 long short_strips(const dq8::Weights& w) { return (w.n + dq8::skinny_cols(1) - 1) / dq8::skinny_cols(1); }
 // 16-column units of a short-K projection (one-wave strips hold two).
 long short_units(const dq8::Weights& w) { return w.g <= 32 ? (w.n + 15) / 16 : 0; }
