@@ -251,9 +251,9 @@ long short_units(const dq8::Weights& w) { return w.g <= 32 ? (w.n + 15) / 16 : 0
 // bytes sets the launch's time (24 rows, graph-replayed: GDN in alone 10.4 ->
 // 8.3 us, gate+up 11.0 -> 8.8 us against 8-unit blocks on fewer CUs).  Two
 // units (one strip) per block at least.  With long-K projections their blocks
-// (one per CU) are the launch's critical path, and short-K blocks on more of
-// their CUs slow them: a layer set with down took 21.1-21.6 us at 8 units per
-// block and 21.5-22.0 us spread out, so such launches keep 8.
+// (one per CU) are the launch's critical path, and spreading the short-K units
+// measured no faster (a layer set with down: 21.1-22.0 us either way), so such
+// launches keep 8.
 #ifndef DQ8_SKINNY_UNITS_MAX
 #define DQ8_SKINNY_UNITS_MAX 7
 #endif
