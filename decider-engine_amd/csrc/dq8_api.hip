@@ -93,10 +93,28 @@ dq8_status from_hip(hipError_t e) {
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
+// Whether work on s would be recorded into a graph.  A failed query counts as
+// capturing: HIP reports an error for the legacy NULL stream while another
+// stream captures in global mode, and an allocation then would invalidate that
+// capture.
 bool capturing(hipStream_t s) {
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-  return hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone;
 }
+
+// While this thread allocates, another stream of the process may be capturing
+// in global mode, where an allocation is an unsafe call that invalidates that
+// capture (and HIP reports the NULL stream as not capturing meanwhile).  The
+// library's own buffers belong to no graph, so the thread switches to relaxed
+// mode around their allocation.
+struct RelaxedCapture {
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  bool swapped;
+  RelaxedCapture() { swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess; }
+  ~RelaxedCapture() {
+    if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
+  }
+};
 
 // Grow a context buffer to at least `bytes`.  Never while `s` is being
 // captured (DQ8_ERR_CAPTURE: nothing is allocated or enqueued).  The old
@@ -108,6 +126,7 @@ dq8_status ensure_buffer(dq8_ctx* ctx, void*& buf, size_t& have, size_t bytes, h
   if (capturing(s)) return DQ8_ERR_CAPTURE;
   const size_t want = std::max(bytes, 2 * have);
   void* fresh = nullptr;
+  RelaxedCapture relaxed;
   hipError_t e = hipMalloc(&fresh, want);
   if (e != hipSuccess) return from_hip(e);
   if (buf) {
@@ -120,6 +139,29 @@ dq8_status ensure_buffer(dq8_ctx* ctx, void*& buf, size_t& have, size_t bytes, h
   }
   buf = fresh;
   have = want;
+  return DQ8_OK;
+}
+// Grow a weight-load staging buffer (load_raw, load_tmp).  Only the weight
+// loads use these, and they synchronize before returning (and refuse a
+// capturing stream), so no queued work or graph can hold the old buffer: it is
+// freed at once and the new one is sized to the request.
+dq8_status ensure_load_buffer(void*& buf, size_t& have, size_t bytes, hipStream_t s) {
+  if (bytes <= have) return DQ8_OK;
+  if (capturing(s)) return DQ8_ERR_CAPTURE;
+  RelaxedCapture relaxed;
+  hipError_t e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return from_hip(e);
+  if (buf) {
+    (void)hipFree(buf);
+    buf = nullptr;
+    have = 0;
+  }
+  e = hipMalloc(&buf, bytes);
+  if (e != hipSuccess) {
+    buf = nullptr;
+    return from_hip(e);
+  }
+  have = bytes;
   return DQ8_OK;
 }
 dq8_status ensure_work(dq8_ctx* ctx, size_t bytes, hipStream_t s) {
@@ -703,7 +745,7 @@ dq8_status quantize_raw_weights(dq8_ctx* ctx, const void* raw, int dtype, size_t
                                 dq8_weights** out) {
   const size_t g = groups_of(k);
   const size_t vbytes = (n * k + 255) & ~(size_t)255;
-  dq8_status st = ensure_buffer(ctx, ctx->load_tmp, ctx->load_tmp_bytes, vbytes + n * g * sizeof(float), s);
+  dq8_status st = ensure_load_buffer(ctx->load_tmp, ctx->load_tmp_bytes, vbytes + n * g * sizeof(float), s);
   if (st != DQ8_OK) return st;
   uint8_t* values = static_cast<uint8_t*>(ctx->load_tmp);
   float* scales = reinterpret_cast<float*>(values + vbytes);
@@ -725,7 +767,7 @@ dq8_status quantize_raw_weights(dq8_ctx* ctx, const void* raw, int dtype, size_t
 template <typename Fill>
 dq8_status load_weights(dq8_ctx* ctx, int dtype, size_t n, size_t k, hipStream_t s, dq8_weights** out, Fill fill) {
   const size_t bytes = n * k * raw_element_bytes(dtype);
-  dq8_status st = ensure_buffer(ctx, ctx->load_raw, ctx->load_raw_bytes, bytes, s);
+  dq8_status st = ensure_load_buffer(ctx->load_raw, ctx->load_raw_bytes, bytes, s);
   if (st != DQ8_OK) return st;
   uint8_t* raw = static_cast<uint8_t*>(ctx->load_raw);
   st = stage_to_device(ctx, raw, bytes, s, fill);
@@ -960,10 +1002,10 @@ dq8_status check_mid(const float* x, size_t m, size_t k, const float* a, size_t 
   return DQ8_OK;
 }
 // Whether the gate and up projections of an FFN can run as one SwiGLU pair
-// launch: the wide kernel (more than 64 rows), no adapters, inputs the kernel
-// reads as they are.
+// launch: a wide-kernel build whose tile shape has the pair mode, the wide
+// kernel (more than 64 rows), no adapters, inputs the kernel reads as they are.
 bool pair_ok(const dq8::Weights& g, const int8_t* q, const float* xs, size_t m) {
-  return kind_of(g, m) == 0 && m > 64 && !needs_pad(g, q) && !needs_xs_pad(g, xs);
+  return dq8::wide_can_pair() && kind_of(g, m) == 0 && m > 64 && !needs_pad(g, q) && !needs_xs_pad(g, xs);
 }
 
 // gate Write into h, then up SwiGlu into h; one launch when pair_ok.

@@ -159,5 +159,8 @@ int skinny_cols(int nseg);  // strip width of a path
 // Block tile of the wide kernel (rows, columns); kColPad is a multiple of the columns.
 int wide_block_rows();
 int wide_block_cols();
+// Whether this build's wide-kernel tile shape has the SwiGLU pair mode (the
+// kernel ignores Proj::pair otherwise).
+bool wide_can_pair();
 
 }  // namespace dq8

@@ -640,6 +640,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // SB-2 newer groups; with SA = 2 < SB the B loads of iteration g-1 (issued
 // after A of group g; B of group g is older).  Groups past the end load
 // clamped operands and the all-zero w-scale row G; they are never computed on.
+// The SwiGLU pair mode needs waves of one 32-row tile and two 32-column tiles
+// (gate and up), two waves across: a block then covers 64 whole h columns.
+constexpr bool wide_pair_shape(int WN, int RT, int CT) { return RT == 1 && CT == 2 && WN == 2; }
 #if DQ8_WIDE_WPE > 0
 #define DQ8_WIDE_ATTR __attribute__((amdgpu_waves_per_eu(DQ8_WIDE_WPE, DQ8_WIDE_WPE)))
 #else
@@ -698,7 +701,7 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   // A SwiGLU pair block covers BN/2 output columns: wave wn's column tile 0
   // is the gate projection's, tile 1 the up projection's, of the same 32
   // outputs (RT == 1, CT == 2 only).
-  constexpr bool CAN_PAIR = !DOTS && !LORA && RT == 1 && CT == 2 && WN == 2;
+  constexpr bool CAN_PAIR = !DOTS && !LORA && wide_pair_shape(WN, RT, CT);
   const bool pair = CAN_PAIR && P.pair;
   const int m0 = mt * BM, n0 = nt * (pair ? BN / 2 : BN);
   const int G = P.g;
@@ -2163,6 +2166,7 @@ int skinny_segments(int g, bool few_strips) { return g <= DQ8_SKINNY_SHORT_MAX_G
 int skinny_cols(int nseg) { return 16 * (nseg == 1 ? DQ8_SKINNY_CT : DQ8_SKINNY_CTL); }
 int wide_block_rows() { return 32 * DQ8_WIDE_RT * DQ8_WIDE_WM; }
 int wide_block_cols() { return 32 * DQ8_WIDE_CT * DQ8_WIDE_WN; }
+bool wide_can_pair() { return wide_pair_shape(DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT); }
 
 hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
   if (b.total_waves == 0) return hipSuccess;

@@ -224,3 +224,42 @@ def test_synchronizing_calls_refuse_capture_and_enqueue_nothing(ctx):
         for a, b in zip((qo, so, h, hq, hs), want):
             assert bits_equal(host(a), b)
     assert int(host(flag)[0]) == 0
+
+
+def test_reserve_while_another_stream_captures_globally_keeps_that_capture():
+    # dq8_reserve grows the workspace from the NULL stream.  While a side
+    # stream captures in global mode, a plain allocation would invalidate that
+    # capture (HIP reports the NULL stream as not capturing meanwhile); the
+    # library allocates in relaxed mode, so the reserve succeeds, the capture
+    # ends and replays, and the reserved workspace then lets a captured
+    # dq8_apply of that size run without allocating.
+    rng = np.random.default_rng(95)
+    c = dq8.Context(0)
+    try:
+        x = torch.zeros(16, dtype=torch.float32, device="cuda")
+        stream = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        status = []
+        with torch.cuda.graph(g, stream=stream, capture_error_mode="global"):
+            x.add_(1.0)
+            status.append(dq8.lib().dq8_reserve(c.handle, 300, 256, 0))
+        assert status == [dq8.OK]
+        for _ in range(2):
+            g.replay()
+        torch.cuda.synchronize()
+        assert host(x).tolist() == [2.0] * 16
+        wv, ws = dq8o.quantize_weights((rng.standard_normal((64, 256)) * 0.05).astype(np.float32))
+        w = c.weights_from_quantized(dev(wv), dev(ws))
+        a0 = rng.standard_normal((300, 256)).astype(np.float32)
+        a, out = dev(a0), torch.zeros((300, 64), dtype=torch.float32, device="cuda")
+        g2 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g2, stream=stream):
+            c.apply(w, a, out=out)
+        g2.replay()
+        torch.cuda.synchronize()
+        assert bits_equal(host(out), dq8o.linear(a0, wv, ws, threads=4))
+        del g, g2
+        w.free()
+    finally:
+        torch.cuda.synchronize()
+        c.close()

@@ -92,3 +92,45 @@ def test_apply_noalloc_rejects_inputs_beyond_its_scratch(ctx):
     assert host(out).tobytes() == host(want).tobytes()
     h.free()
     h2.free()
+
+
+def test_apply_noalloc_captures_on_a_fresh_context_and_replays_bit_exact():
+    # A new context has no workspace at all, so dq8_apply would have to
+    # allocate (and refuses under capture); dq8_apply_noalloc captures as it
+    # is and its replays equal the oracle.  Shapes: a 128-row small call whose
+    # int8 path runs as skinny row chunks over the scratch-held inputs, a
+    # 2048-row wide launch, and a 24-row skinny call.
+    rng = np.random.default_rng(909)
+    c = dq8.Context(0)
+    try:
+        cases = [(128, 2048, 2048), (2048, 2048, 512), (24, 6144, 256)]
+        stream = torch.cuda.Stream()
+        for m, k, n in cases:
+            x0 = rng.standard_normal((m, k)).astype(np.float32)
+            wv, ws = dq8o.quantize_weights((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+            bias0 = rng.standard_normal(n).astype(np.float32)
+            h = c.weights_from_quantized(dev(wv), dev(ws))
+            x, bias = dev(x0), dev(bias0)
+            out = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            status = []
+            with torch.cuda.graph(g, stream=stream):
+                status.append(noalloc(c, h, x, out, bias=bias))
+            assert status == [dq8.OK], (m, k, n)
+            want = dq8o.linear(x0, wv, ws, bias=bias0, threads=8)
+            for replay in range(3):
+                out.fill_(-1.0)
+                torch.cuda.synchronize()
+                g.replay()
+                torch.cuda.synchronize()
+                assert same_bits(host(out), want), (m, k, n, replay)
+                # eager work between the replays, on the same shared scratch
+                eager = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+                assert noalloc(c, h, dev(rng.standard_normal((m, k)).astype(np.float32)), eager) == dq8.OK
+                torch.cuda.synchronize()
+            del g
+            h.free()
+    finally:
+        torch.cuda.synchronize()
+        c.close()
