@@ -12,8 +12,9 @@ the projection kernels.
     products are subnormal or underflow;
   - non-finite weights rejected by every weight entry point (weights.rs:170-187).
 
-Full-size results are checked against the oracle on sampled rows (rows are
-independent: each is quantized and multiplied on its own) and, for the rest,
+Full-size results are checked against the oracle on sampled rows, at least one
+in every 64-row tile (rows are independent: each is quantized and multiplied
+on its own) and, for the rest,
 through properties that hold bit for bit: a row permutation of the input
 permutes the output rows, and splitting the weight rows over two handles gives
 the same columns.
@@ -62,6 +63,15 @@ def student(rng, rows, width):
     z = rng.standard_normal((rows, width))
     chi = rng.chisquare(3, size=(rows, width))
     return (z / np.sqrt(chi / 3)).astype(np.float32)
+
+
+def tile_rows(rng, m, extra=8, tile=64):
+    """Oracle rows of a full-size check: one random row in every 64-row tile
+    of the output (each wide launch's row tiles, and with them every XCD
+    region and column chunk of the tile walk), the first and last rows, and a
+    few more at random."""
+    rows = [int(rng.integers(t, min(t + tile, m))) for t in range(0, m, tile)]
+    return np.unique(np.r_[rows, 0, m - 1, rng.choice(m, size=extra, replace=False)])
 
 
 def weights(ctx, rng, n, k):
@@ -170,8 +180,7 @@ def test_layer_projection_set_4096_tokens_with_outlier_channels(ctx):
     for nm in ("gdn_in", "o", "gdn_out"):
         ctx.linear(W[nm][2], *qs[src[nm]], out=outs[nm])
     got = {nm: host(o) for nm, o in outs.items()}
-    rows = np.sort(rng.choice(m, size=48, replace=False))
-    rows[-1] = m - 1  # the last row tile
+    rows = tile_rows(rng, m)
     for nm, _ in LAYER3:
         wv, ws, _ = W[nm]
         want = dq8o.linear(inputs[nm][rows], wv, ws, threads=16)
@@ -218,8 +227,7 @@ def test_stack_gdn_layer_2048_tokens_student_t(ctx):
     W = {nm: weights(ctx, rng, n, k) for nm, n, k in
          [("in", 8224, 2048), ("out", 2048, 2048), ("gate", 6144, 2048), ("up", 6144, 2048), ("down", 2048, 6144)]}
     x, xm, xf = (student(rng, m, 2048) for _ in range(3))
-    rows = np.sort(rng.choice(m, size=40, replace=False))
-    rows[0], rows[-1] = 0, m - 1
+    rows = tile_rows(rng, m)
     q, s = ctx.quantize(dev(x))
     mixer = host(ctx.linear(W["in"][2], q, s))
     assert bits_equal(mixer[rows], dq8o.linear(x[rows], W["in"][0], W["in"][1], threads=16)), "GDN in"
@@ -236,8 +244,7 @@ def test_stack_gqa_layer_2048_tokens_student_t(ctx):
          [("q", 2048, 2048), ("k", 512, 2048), ("v", 512, 2048), ("o", 2048, 2048), ("gate", 6144, 2048),
           ("up", 6144, 2048), ("down", 2048, 6144)]}
     x, xo, xf = (student(rng, m, 2048) for _ in range(3))
-    rows = np.sort(rng.choice(m, size=40, replace=False))
-    rows[-1] = m - 1
+    rows = tile_rows(rng, m)
     q, s = ctx.quantize(dev(x))
     outs = {nm: torch.zeros((m, W[nm][0].shape[0]), dtype=torch.float32, device="cuda") for nm in ("q", "k", "v")}
     ctx.linear_batch([dq8.Item(W[nm][2], q, s, outs[nm]) for nm in ("q", "k", "v")])

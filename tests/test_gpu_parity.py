@@ -51,6 +51,13 @@ def make_x(rng, rows, width, kind="normal"):
     return x
 
 
+def tile_rows(rng, m, extra=8, tile=64):
+    """Oracle rows of a full-size check: one random row in every 64-row tile,
+    the first and last rows, and a few more at random."""
+    rows = [int(rng.integers(t, min(t + tile, m))) for t in range(0, m, tile)]
+    return np.unique(np.r_[rows, 0, m - 1, rng.choice(m, size=extra, replace=False)])
+
+
 def make_w(rng, n, k):
     return (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
 
@@ -926,7 +933,7 @@ def test_ffn_full_size_sampled_rows(ctx, kind):
     # One FFN of the 24-layer stack at full size: 2048 tokens, 2048 -> 6144
     # gate/up (one launch of 3072 blocks storing h), h re-quantized, 6144 ->
     # 2048 down Add (qwen.rs:486-492).  Rows are independent, so the oracle
-    # recomputes 24 sampled rows of h and of the residual.
+    # recomputes sampled rows of h and of the residual, one in every 64-row tile.
     rng = np.random.default_rng(6144 + len(kind))
     m, hidden, inter = 2048, 2048, 6144
     x = make_x(rng, m, hidden, kind)
@@ -939,7 +946,7 @@ def test_ffn_full_size_sampled_rows(ctx, kind):
     resid0 = rng.standard_normal((m, hidden)).astype(np.float32)
     resid = dev(resid0.copy())
     h = host(ctx.ffn(G, U, D, q, s, resid, biases=(dev(gb), None, None)))
-    rows = np.unique(np.r_[0, m - 1, rng.choice(m, size=22, replace=False)])
+    rows = tile_rows(rng, m)
     gate = dq8o.linear(x[rows], gv, gs, bias=gb, threads=8)
     want_h = dq8o.linear(x[rows], uv, us, result=gate, epilogue=2, threads=8)
     assert bits_equal(h[rows], want_h)
@@ -949,7 +956,8 @@ def test_ffn_full_size_sampled_rows(ctx, kind):
 
 def test_full_size_gdn_in_projection_properties(ctx):
     # The headline stack's largest projection at full size (2048 tokens x
-    # 2048 -> 8224, 2112 wide blocks).  The oracle checks 64 sampled rows; the
+    # 2048 -> 8224, 2112 wide blocks).  The oracle checks sampled rows, one in
+    # every 64-row tile and 32 more; the
     # rest is pinned by properties that hold bit for bit: rows are independent
     # (a row permutation of x permutes the result), and output columns are
     # independent (the weights split in two launches give the same columns).
@@ -960,7 +968,7 @@ def test_full_size_gdn_in_projection_properties(ctx):
     h = ctx.weights_from_quantized(dev(wv), dev(ws))
     q, s = ctx.quantize(dev(x))
     full = host(ctx.linear(h, q, s))
-    rows = rng.choice(m, size=64, replace=False)
+    rows = tile_rows(rng, m, extra=32)
     assert bits_equal(full[rows], dq8o.linear(x[rows], wv, ws, threads=8))
     perm = rng.permutation(m)
     qp, sp = ctx.quantize(dev(x[perm]))
