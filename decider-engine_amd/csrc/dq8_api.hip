@@ -286,21 +286,20 @@ constexpr long kSkinnyFewStrips = 160;
 long short_strips(const dq8::Weights& w) { return (w.n + dq8::skinny_cols(1) - 1) / dq8::skinny_cols(1); }
 // 16-column units of a short-K projection (one-wave strips hold two).
 long short_units(const dq8::Weights& w) { return w.g <= 32 ? (w.n + 15) / 16 : 0; }
-// Units per block of a skinny launch's short-K projections (8: whole
-// 32-column strips, 4 per block).  Without long-K projections in the launch,
-// the units spread over about one block per CU, at most 7 per block:
+// Units per block of a skinny launch's short-K projections.  The units spread
+// over about one block per CU, at most 7 per block, two (one strip) at least:
 // each CU streams its bytes at a limited rate, so the CU holding the most
 // bytes sets the launch's time (24 rows, graph-replayed: GDN in alone 10.4 ->
-// 8.3 us, gate+up 11.0 -> 8.8 us against 8-unit blocks on fewer CUs).  Two
-// units (one strip) per block at least.  With long-K projections their blocks
-// (one per CU) are the launch's critical path, and spreading the short-K units
-// measured no faster (a layer set with down: 21.1-22.0 us either way), so such
-// launches keep 8.
+// 8.3 us, gate+up 11.0 -> 8.8 us against 8-unit blocks of 4 whole strips on
+// fewer CUs).  Launches with long-K projections deal them the same way: the
+// 24-row 9-projection layer set went 3.42 -> 3.51 TB/s per question
+// (graph-replayed, 5 rotating weight copies).  (8 would select blocks of 4
+// whole 32-column strips, one per wave.)
 #ifndef DQ8_SKINNY_UNITS_MAX
 #define DQ8_SKINNY_UNITS_MAX 7
 #endif
-int units_per_block(long units, bool has_long) {
-  return has_long ? 8 : (int)std::min((long)DQ8_SKINNY_UNITS_MAX, std::max(2L, (units + 255) / 256));
+int units_per_block(long units, bool /*has_long*/) {
+  return (int)std::min((long)DQ8_SKINNY_UNITS_MAX, std::max(2L, (units + 255) / 256));
 }
 
 // Row chunks for the skinny kernel.  Up to 64 rows (rows layout) always run as
