@@ -265,22 +265,22 @@ def main():
             calls.append(quant(L["mix"], qx, sx, HIDDEN))
             proj(L, "out" if L["kind"] == "gdn" else "o", L["mix"], qx, sx, proj_out, dq8.WRITE, mids["a"], HIDDEN)
             calls.append(quant(L["ffn"], qx, sx, HIDDEN))
+            # gate and up in one launch storing h and its quantization for down (qwen.rs:489-491),
+            # each with its adapter when the leg has them, then down Add
+            ops = sum(2 * M * L[n].n * L[n].k for n in ("gate", "up"))
+            lg = lu = None
             if with_lora:  # gate and up share their input: one grouped launch of their middle products
                 calls.append(mid_batch_call([(L["ffn"], lora_of(L, "gate")[0], mids["b"], HIDDEN),
                                              (L["ffn"], lora_of(L, "up")[0], mids["c"], HIDDEN)]))
-                proj(L, "gate", L["ffn"], qx, sx, gate, dq8.WRITE, mids["b"], HIDDEN, with_mid=False)
-                proj(L, "up", L["ffn"], qx, sx, gate, dq8.SWIGLU, mids["c"], HIDDEN, with_mid=False)
-                calls.append(quant(gate, qf, sf, FFN_DIM))
-                proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
-            else:
-                # gate and up in one launch storing h and its quantization for down (qwen.rs:489-491),
-                # then down Add
-                ops = sum(2 * M * L[n].n * L[n].k for n in ("gate", "up"))
-                calls.append(("linear", lib.dq8_ffn_gate_up, (ctx.handle, L["gate"].handle, L["up"].handle,
-                                                              qx.data_ptr(), sx.data_ptr(), M, None, None,
-                                                              gate.data_ptr(), qf.data_ptr(), sf.data_ptr(),
-                                                              flag.data_ptr(), sh), (0, ops)))
-                proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
+                lg = dq8._Lora(mids["b"].data_ptr(), lora_of(L, "gate")[1].data_ptr(), rank, 2.0)
+                lu = dq8._Lora(mids["c"].data_ptr(), lora_of(L, "up")[1].data_ptr(), rank, 2.0)
+                keep.extend((lg, lu))
+                lg, lu = ctypes.byref(lg), ctypes.byref(lu)
+            calls.append(("linear", lib.dq8_ffn_gate_up_lora, (ctx.handle, L["gate"].handle, L["up"].handle,
+                                                               qx.data_ptr(), sx.data_ptr(), M, None, None, lg, lu,
+                                                               gate.data_ptr(), qf.data_ptr(), sf.data_ptr(),
+                                                               flag.data_ptr(), sh), (0, ops)))
+            proj(L, "down", gate, qf, sf, resid, dq8.ADD, mids["a"], FFN_DIM)
         layer_bounds.append(len(calls))
         return calls
 

@@ -222,6 +222,11 @@ void fill_proj(dq8::Proj& p, const dq8::Weights& w, const int8_t* q, int ldq, co
   p.hs = nullptr;
   p.hflag = nullptr;
   p.pair = 0;
+  p.lmid2 = nullptr;
+  p.lb2 = nullptr;
+  p.lora2 = 0;
+  p.rank2 = 0;
+  p.lscale2 = 0.0f;
 }
 
 // Wide kernel: split the tile grid into gm x gn regions, gm * gn = 8, one per
@@ -530,27 +535,33 @@ dq8_status run_linear(dq8_ctx* ctx, const dq8_linear_item* items, size_t count, 
   return DQ8_OK;
 }
 
-// One layer's gate and up projections (same shape, shared quantized input,
-// no adapters) in one wide launch that stores h = silu(gate + bias) * (up +
-// bias2) into h [m][n] and, as qout asks, quantizes h in the same launch
+// One layer's gate and up projections (same shape, shared quantized input)
+// in one wide launch that stores h = silu(gate + bias + adapter) * (up + bias2
+// + adapter2) into h [m][n] and, as qout asks, quantizes h in the same launch
 // (q [m][n], scales [m][ceil(n/64)], the non-finite flag).  The results equal
 // the separate Write and SwiGlu launches and k_quantize bit for bit: each
 // output's arithmetic is unchanged, only the two tiles of one output sit in
-// one wave, and a block holds whole 64-column groups of h.
+// one wave, and a block holds whole 64-column groups of h.  gate_lora and
+// up_lora are NULL or pass pair_lora_ok.
 dq8_status run_pair(dq8_ctx* ctx, const dq8::Weights& g, const dq8::Weights& u, const int8_t* q, const float* xs,
-                    size_t m, const float* gate_bias, const float* up_bias, float* h, const QOut* qout,
-                    hipStream_t s) {
+                    size_t m, const float* gate_bias, const float* up_bias, const dq8_lora* gate_lora,
+                    const dq8_lora* up_lora, float* h, const QOut* qout, hipStream_t s) {
   (void)ctx;
   dq8::Batch b;
   b.count = 1;
   b.total_waves = 0;
-  b.any_lora = 0;
+  b.any_lora = gate_lora != nullptr || up_lora != nullptr;
   b.unless = nullptr;
   dq8::Proj& p = b.p[0];
-  fill_proj(p, g, q, g.k, xs, g.g, m, gate_bias, h, nullptr, DQ8_ROWS, DQ8_WRITE, nullptr);
+  fill_proj(p, g, q, g.k, xs, g.g, m, gate_bias, h, nullptr, DQ8_ROWS, DQ8_WRITE, gate_lora);
   p.wt2 = u.values;
   p.wst2 = u.scales;
   p.bias2 = up_bias;
+  p.lmid2 = up_lora ? up_lora->mid : nullptr;
+  p.lb2 = up_lora ? up_lora->b : nullptr;
+  p.lora2 = up_lora != nullptr;
+  p.rank2 = up_lora ? (int)up_lora->rank : 0;
+  p.lscale2 = up_lora ? up_lora->scale : 0.0f;
   if (qout) {
     p.hq = qout->q;
     p.hs = qout->scales;
@@ -1002,17 +1013,24 @@ dq8_status check_mid(const float* x, size_t m, size_t k, const float* a, size_t 
 }
 // Whether the gate and up projections of an FFN can run as one SwiGLU pair
 // launch: a wide-kernel build whose tile shape has the pair mode, the wide
-// kernel (more than 64 rows), no adapters, inputs the kernel reads as they are.
+// kernel (more than 64 rows), inputs the kernel reads as they are.
 bool pair_ok(const dq8::Weights& g, const int8_t* q, const float* xs, size_t m) {
   return dq8::wide_can_pair() && kind_of(g, m) == 0 && m > 64 && !needs_pad(g, q) && !needs_xs_pad(g, xs);
+}
+// Adapters the pair launch's epilogue takes: rank 0, or rank 16 with 16-byte
+// aligned mid and b (the rank of the reference's checkpoints); any other goes
+// to the separate gate and up launches.
+bool pair_lora_ok(const dq8_lora* l) {
+  return !l || l->rank == 0 ||
+         (l->rank == 16 && ((uintptr_t)l->mid & 15) == 0 && ((uintptr_t)l->b & 15) == 0);
 }
 
 // gate Write into h, then up SwiGlu into h; one launch when pair_ok.
 dq8_status gate_up(dq8_ctx* ctx, const dq8_weights* gate, const dq8_weights* up, const int8_t* q, const float* xs,
                    size_t m, const float* gate_bias, const float* up_bias, const dq8_lora* gate_lora,
                    const dq8_lora* up_lora, float* h, const QOut* qout, hipStream_t s) {
-  if (!gate_lora && !up_lora && pair_ok(gate->w, q, xs, m))
-    return run_pair(ctx, gate->w, up->w, q, xs, m, gate_bias, up_bias, h, qout, s);
+  if (pair_ok(gate->w, q, xs, m) && pair_lora_ok(gate_lora) && pair_lora_ok(up_lora))
+    return run_pair(ctx, gate->w, up->w, q, xs, m, gate_bias, up_bias, gate_lora, up_lora, h, qout, s);
   dq8_linear_item gi = {gate, q, xs, m, gate_bias, h, DQ8_ROWS, DQ8_WRITE, gate_lora};
   dq8_status st = run_linear(ctx, &gi, 1, nullptr, s);
   if (st != DQ8_OK) return st;
@@ -1090,28 +1108,38 @@ dq8_status dq8_linear_batch(dq8_ctx* ctx, const dq8_linear_item* items, size_t c
   return run_linear(ctx, items, count, nullptr, (hipStream_t)stream);
 }
 
-dq8_status dq8_ffn_gate_up(dq8_ctx* ctx, const dq8_weights* gate, const dq8_weights* up, const int8_t* q,
-                           const float* scales, size_t m, const float* gate_bias, const float* up_bias, float* h,
-                           int8_t* h_q, float* h_scales, uint32_t* nonfinite, void* stream) {
+dq8_status dq8_ffn_gate_up_lora(dq8_ctx* ctx, const dq8_weights* gate, const dq8_weights* up, const int8_t* q,
+                                const float* scales, size_t m, const float* gate_bias, const float* up_bias,
+                                const dq8_lora* gate_lora, const dq8_lora* up_lora, float* h, int8_t* h_q,
+                                float* h_scales, uint32_t* nonfinite, void* stream) {
   if (!ctx || !gate || !up) return DQ8_ERR_ARG;
   if (m == 0) return DQ8_OK;
   if (gate->w.k != up->w.k || gate->w.n != up->w.n) return DQ8_ERR_SHAPE;
   dq8_status st = check_item_args(gate, q, scales, m, h, DQ8_ROWS, DQ8_WRITE);
+  if (st == DQ8_OK) st = check_lora(gate_lora);
+  if (st == DQ8_OK) st = check_lora(up_lora);
   if (st != DQ8_OK) return st;
   if (gate->w.device != ctx->device || up->w.device != ctx->device) return DQ8_ERR_ARG;
   if ((h_q == nullptr) != (h_scales == nullptr)) return DQ8_ERR_ARG;
   DeviceGuard guard(ctx->device);
   hipStream_t s = (hipStream_t)stream;
-  if (!h_q) return gate_up(ctx, gate, up, q, scales, m, gate_bias, up_bias, nullptr, nullptr, h, nullptr, s);
+  if (!h_q) return gate_up(ctx, gate, up, q, scales, m, gate_bias, up_bias, gate_lora, up_lora, h, nullptr, s);
   if (!nonfinite && capturing(s)) return DQ8_ERR_CAPTURE;  // it would synchronize
   if (!nonfinite) {
     hipError_t e = dq8::launch_fill_u32(ctx->flag, 0, s);
     if (e != hipSuccess) return from_hip(e);
   }
   QOut qo = {h_q, h_scales, nonfinite ? nonfinite : ctx->flag};
-  st = gate_up(ctx, gate, up, q, scales, m, gate_bias, up_bias, nullptr, nullptr, h, &qo, s);
+  st = gate_up(ctx, gate, up, q, scales, m, gate_bias, up_bias, gate_lora, up_lora, h, &qo, s);
   if (st != DQ8_OK || nonfinite) return st;
   return finish_nonfinite(ctx, s);
+}
+
+dq8_status dq8_ffn_gate_up(dq8_ctx* ctx, const dq8_weights* gate, const dq8_weights* up, const int8_t* q,
+                           const float* scales, size_t m, const float* gate_bias, const float* up_bias, float* h,
+                           int8_t* h_q, float* h_scales, uint32_t* nonfinite, void* stream) {
+  return dq8_ffn_gate_up_lora(ctx, gate, up, q, scales, m, gate_bias, up_bias, nullptr, nullptr, h, h_q, h_scales,
+                              nonfinite, stream);
 }
 
 dq8_status dq8_linear_f32in(dq8_ctx* ctx, const dq8_weights* w, const float* x, size_t m, const float* bias,

@@ -64,6 +64,13 @@ struct Proj {
   float* hs;
   uint32_t* hflag;
   int pair;
+  // The up projection's LoRA adapter in a pair launch (lmid/lb/rank/lscale of
+  // the fields above are the gate's).
+  const float* lmid2;
+  const float* lb2;
+  int lora2;
+  int rank2;
+  float lscale2;
 };
 
 // Division by a fixed d >= 1 for 0 <= n < 2^31 without a divide (Granlund and

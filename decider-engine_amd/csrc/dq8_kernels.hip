@@ -266,6 +266,68 @@ __device__ __forceinline__ V lora_term16(const V& base, const V& zero, int rank,
   return base + scale * (sum + zero);
 }
 
+// LDS staging of lora_block32: 64 rows of kLoraRow floats per wave.
+constexpr int kLoraRow = 17;
+constexpr int kLoraStage = 64 * kLoraRow * 4;
+
+// Adapter term of one 32 x 32 block of a wave (rows mw .. mw+31, columns cb ..
+// cb+31; element v of lane l at row mw + 8(v/4) + 4(l/32) + v%4, column
+// cb + l%32): base + scale * (dot_scores(mid[row], b[col]) + 0.0), the same
+// arithmetic as the adapter epilogue of k_linear_wide.  For rank 16 the wave
+// first copies its 32 mid rows and 32 b rows into its own kLoraStage bytes of
+// LDS (lw; rows padded to 17 floats, so the 32 b rows one operand read touches
+// sit in distinct banks and every read is a base register plus an immediate
+// offset), then forms the products with v_mfma_f32_4x4x1_16b_f32 in 4 slices
+// of 4 rows.  Only ranks 0 and 16 (with
+// 16-byte aligned mid and b) come here: the host sends other adapters of a
+// gate/up pair to separate launches, whose epilogue takes any rank.
+__device__ __forceinline__ v16f lora_block32(v16f base, const float* lmid, const float* lb, int rank, float scale,
+                                             int m, int n, int mw, int cb, int lane, float* lw) {
+  v16f zero16;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) zero16[i] = 0.0f;
+  if (rank == 0) return base + scale * (zero16 + zero16);  // no products: a +0.0 dot
+  const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  float* lmw = lw;                  // rows 0-31: mid
+  float* lbw = lw + 32 * kLoraRow;  // rows 32-63: b
+  // Both operand runs are contiguous (32 * 16 floats each); rows past m or n
+  // read the last row instead.
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int e = 64 * t + lane;  // float4 index: row e/4, inputs 4(e%4)..+3
+    const v4f vm = *reinterpret_cast<const v4f*>(lmid + (size_t)min(mw + (e >> 2), m - 1) * 16 + 4 * (e & 3));
+    const v4f vb = *reinterpret_cast<const v4f*>(lb + (size_t)min(cb + (e >> 2), n - 1) * 16 + 4 * (e & 3));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      lmw[(e >> 2) * kLoraRow + 4 * (e & 3) + q] = vm[q];
+      lbw[(e >> 2) * kLoraRow + 4 * (e & 3) + q] = vb[q];
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's copies are visible to it
+  const int c = lane & 31;
+  const float* rb = lbw + kLoraRow * c;
+  const float* rm0 = lmw + kLoraRow * (4 * (lane >> 5) + (lane & 3));
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float* rm = rm0 + 8 * kLoraRow * u;  // row 8u + 4(lane/32) + lane%4
+    auto prod = [&](int i) { return mfma_k1_4(rm[i], rb[i], zero4); };
+    v4f su;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const v4f ln = prod(i) + prod(8 + i);
+      su = i == 0 ? ln : su + ln;
+      // keeps the scheduler from issuing every product of the block at once:
+      // the pair kernel holds both 32 x 32 accumulators here
+      if ((i & 1) == 1) __builtin_amdgcn_sched_barrier(0);
+    }
+    // a slice's 4 elements are final: combine them now (elementwise, so the
+    // same arithmetic as combining the whole block at the end)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) base[4 * u + v] = base[4 * u + v] + scale * (su[v] + 0.0f);
+  }
+  return base;
+}
+
 // ---------------------------------------------------------------------------
 // Stored weight elements (Data::read, weights.rs:147-195): little-endian F32,
 // BF16 (the upper half of an F32) or F16.  Both 16-bit decodings are exact:
@@ -696,7 +758,7 @@ constexpr bool wide_pair_shape(int WN, int RT, int CT) { return RT == 1 && CT ==
 #else
 #define DQ8_WIDE_ATTR
 #endif
-template <int WM, int WN, int RT, int CT, int SA, int SB, int XCH, int SWZ, bool DOTS, bool LORA>
+template <int WM, int WN, int RT, int CT, int SA, int SB, int XCH, int SWZ, bool DOTS, bool LORA, bool PL = false>
 __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batch b) {
   constexpr int NW = WM * WN, WR = 32 * RT, WC = 32 * CT;
   constexpr int BM = WR * WM, BN = WC * WN;
@@ -743,13 +805,16 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int blk = blockIdx.x;
-  const Proj P = b.p[find_proj(b, blk)];
+  const int pidx = find_proj(b, blk);
+  const Proj P = b.p[pidx];
   int mt, nt;
   tile_of(P, blk - P.wave_begin, (P.m + BM - 1) / BM, mt, nt);
   // A SwiGLU pair block covers BN/2 output columns: wave wn's column tile 0
   // is the gate projection's, tile 1 the up projection's, of the same 32
   // outputs (RT == 1, CT == 2 only).
-  constexpr bool CAN_PAIR = !DOTS && !LORA && wide_pair_shape(WN, RT, CT);
+  // The pair mode is compiled into the plain kernels and, with adapters, only
+  // into the PL ones (its epilogue would raise every adapter launch's registers).
+  constexpr bool CAN_PAIR = !DOTS && wide_pair_shape(WN, RT, CT) && (!LORA || PL);
   const bool pair = CAN_PAIR && P.pair;
   const int m0 = mt * BM, n0 = nt * (pair ? BN / 2 : BN);
   const int G = P.g;
@@ -934,18 +999,56 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   wait_vmcnt<0>();
   if constexpr (CAN_PAIR) {
     if (pair) {
-      // y = s + bias for both projections (tensor.rs:437), then the up
-      // projection's SwiGlu store over the gate's result (tensor.rs:96-99,
-      // qwen.rs:489-490): h = silu(y_gate) * y_up, each op rounded.
+      // y = s + bias for both projections (tensor.rs:437) and their adapter
+      // terms, then the up projection's SwiGlu store over the gate's result
+      // (tensor.rs:96-99, qwen.rs:489-490): h = silu(y_gate) * y_up, each op
+      // rounded.
       const int mw = m0 + WR * wm, col = n0 + 32 * wn + (lane & 31);
       const float bg = P.bias != nullptr && col < P.n ? P.bias[col] : 0.0f;
       const float bu = P.bias2 != nullptr && col < P.n ? P.bias2[col] : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        s[0][v] = s[0][v] + bg;
+        s[0][16 + v] = s[0][16 + v] + bu;
+      }
+      if constexpr (LORA) {
+        // then each projection's adapter term (Adapter::combine, tensor.rs:109-117,
+        // after the bias: 438): gate's on column tile 0, up's on tile 1, in this
+        // wave's kLoraStage bytes of the idle ring
+        static_assert(sizeof(Ring) >= NW * kLoraStage, "adapter staging fits the ring");
+        if (P.lora || P.lora2) {
+          __builtin_amdgcn_sched_barrier(0);
+          lds_barrier();  // every wave is done reading the ring
+          float* lw = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(&ring) + wid * kLoraStage);
+#pragma unroll
+          for (int bk = 0; bk < 2; ++bk) {
+            if (bk == 0 ? !P.lora : !P.lora2) continue;  // uniform (lora2 is read with the other pair fields)
+            v16f base;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) base[v] = s[0][16 * bk + v];
+            if (bk == 0) {
+              base = lora_block32(base, P.lmid, P.lb, P.rank, P.lscale, P.m, P.n, mw, n0 + 32 * wn, lane, lw);
+            } else {
+              // the up adapter's fields, read here rather than kept in registers
+              // across the main loop (the empty asm keeps the loads from moving up)
+              int pi = __builtin_amdgcn_readfirstlane(pidx);
+              asm volatile("" : "+s"(pi));
+              const Proj* pp = &b.p[pi];
+              base = lora_block32(base, pp->lmid2, pp->lb2, pp->rank2, pp->lscale2, P.m, P.n, mw, n0 + 32 * wn,
+                                  lane, lw);
+            }
+#pragma unroll
+            for (int v = 0; v < 16; ++v) s[0][16 * bk + v] = base[v];
+            __builtin_amdgcn_sched_barrier(0);  // one adapter block's operands live at a time
+          }
+        }
+      }
       const ExpTab T = exp_table(lane);
       float hv[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = mw + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const float yg = s[0][v] + bg, yu = s[0][16 + v] + bu;
+        const float yg = s[0][v], yu = s[0][16 + v];
         hv[v] = silu_wave(yg, T) * yu;
         if (row < P.m && col < P.n) st_out(P.out + (size_t)row * P.n + col, hv[v]);
         if ((v & 3) == 3) __builtin_amdgcn_sched_barrier(0);
@@ -2238,6 +2341,13 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
   k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, SA, SB, X, DQ8_WIDE_SWZ, D, L> \
       <<<b.total_waves, threads, 0, s>>>(b)
     constexpr int S0 = DQ8_WIDE_STAGES, S1 = DQ8_WIDE_STAGES + 1, X = DQ8_WIDE_XCH;
+    bool pair_lora = false;
+    for (int i = 0; i < b.count; ++i) pair_lora |= b.p[i].pair && (b.p[i].lora || b.p[i].lora2);
+    if (pair_lora) {  // a SwiGLU pair with adapters
+      k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, 2, 3, 8, DQ8_WIDE_SWZ, false, true, true>
+          <<<b.total_waves, threads, 0, s>>>(b);
+      return hipGetLastError();
+    }
     if (dots) DQ8_WIDE(S0, S0, X, true, false);
 #if DQ8_WIDE_SPLIT == 0
     else if (lora) deep ? DQ8_WIDE(S1, S1, X, false, true) : DQ8_WIDE(S0, S0, X, false, true);

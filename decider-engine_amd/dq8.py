@@ -132,6 +132,7 @@ def lib() -> ctypes.CDLL:
         "dq8_linear_q": ([_vp, _vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _vp, _vp, _vp, _vp], _i),
         "dq8_ffn": ([_vp, ctypes.POINTER(_FfnWeights), _vp, _vp, _sz, _vp, _vp, _vp, _vp], _i),
         "dq8_ffn_gate_up": ([_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
+        "dq8_ffn_gate_up_lora": ([_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], _i),
         "dq8_group_dots": ([_vp, _vp, _vp, _sz, _vp, _vp], _i),
         "dq8_status_string": ([_i], ctypes.c_char_p),
         "dq8_linear_fp32": ([_vp, _vp, _vp, _sz, _vp, ctypes.POINTER(_Lora), _vp, _i, _i, _vp], _i),
@@ -488,11 +489,12 @@ class Context:
         return h
 
     def ffn_gate_up(self, gate: Weights, up: Weights, q, scales, h=None, biases=(None, None), quantize=False,
-                    nonfinite=None):
+                    nonfinite=None, loras=(None, None)):
         """h = silu(gate(x) + gate_bias) * (up(x) + up_bias) (qwen.rs:489-490), the gate Write and up SwiGlu
-        stores of one FFN in one call.  Returns h [m][n], or with quantize=True (h, h_q, h_scales): h also
-        quantized for the down projection, as dq8_quantize(h) would; raises NonFinite like dq8_quantize unless
-        `nonfinite` (a zeroed uint32 device scalar) is given."""
+        stores of one FFN in one call, each projection with its LoRA adapter when loras gives one (Lora, with
+        the adapter's middle product computed).  Returns h [m][n], or with quantize=True (h, h_q, h_scales): h
+        also quantized for the down projection, as dq8_quantize(h) would; raises NonFinite like dq8_quantize
+        unless `nonfinite` (a zeroed uint32 device scalar) is given."""
         torch = _torch()
         self._dev(q, torch.int8, name="q")
         m, k = q.shape
@@ -504,9 +506,11 @@ class Context:
         if quantize:
             hq = torch.empty((m, up.n), dtype=torch.int8, device=self.device)
             hs = torch.empty((m, groups(up.n)), dtype=torch.float32, device=self.device)
-        _check(lib().dq8_ffn_gate_up(self.handle, gate.handle, up.handle, q.data_ptr(), scales.data_ptr(), m,
-                                     _ptr(biases[0]), _ptr(biases[1]), h.data_ptr(), _ptr(hq), _ptr(hs),
-                                     _ptr(nonfinite), _stream(self.device)), "dq8_ffn_gate_up")
+        lo = [self._lora(lr, m, w.n) if lr is not None else None for lr, w in zip(loras, (gate, up))]
+        lp = [ctypes.byref(x) if x is not None else None for x in lo]
+        _check(lib().dq8_ffn_gate_up_lora(self.handle, gate.handle, up.handle, q.data_ptr(), scales.data_ptr(), m,
+                                          _ptr(biases[0]), _ptr(biases[1]), lp[0], lp[1], h.data_ptr(), _ptr(hq),
+                                          _ptr(hs), _ptr(nonfinite), _stream(self.device)), "dq8_ffn_gate_up_lora")
         return (h, hq, hs) if quantize else h
 
     def linear_f32in(self, w: Weights, x, out=None, bias=None, layout=ROWS, epilogue=WRITE):

@@ -250,6 +250,18 @@ typedef struct dq8_ffn_weights {
 dq8_status dq8_ffn_gate_up(dq8_ctx *ctx, const dq8_weights *gate, const dq8_weights *up, const int8_t *q,
                            const float *scales, size_t m, const float *gate_bias, const float *up_bias, float *h,
                            int8_t *h_q, float *h_scales, uint32_t *nonfinite, void *stream);
+/* dq8_ffn_gate_up with the projections' LoRA adapters (either may be NULL):
+ * the gate Write and up SwiGlu apply calls of Linear::apply_into_shared with
+ * adapters (weights.rs:492-520; Adapter::combine, tensor.rs:109-117, after the
+ * bias, tensor.rs:437-438), each adapter's middle product `mid` already
+ * computed (dq8_lora_mid / dq8_lora_mid_batch).  The one-launch path takes
+ * adapters of rank 0, and of rank 16 (the reference checkpoints' rank) with
+ * 16-byte aligned mid and b: h is then still stored (and quantized) once.
+ * Other adapters run as the two separate launches, with the same bits. */
+dq8_status dq8_ffn_gate_up_lora(dq8_ctx *ctx, const dq8_weights *gate, const dq8_weights *up, const int8_t *q,
+                                const float *scales, size_t m, const float *gate_bias, const float *up_bias,
+                                const dq8_lora *gate_lora, const dq8_lora *up_lora, float *h, int8_t *h_q,
+                                float *h_scales, uint32_t *nonfinite, void *stream);
 /* One layer's FFN chain on the device (qwen.rs:486-492):
  *   h = gate(x)                          Write            (Linear::apply_shared)
  *   h = silu(h) * up(x)                  SwiGlu           (apply_into_shared)

@@ -1019,6 +1019,81 @@ def test_ffn_gate_up_quantize_edge_groups(ctx):
     assert int(host(flag)[0]) == 0
 
 
+def _adapter(ctx, rng, m, k, n, rank, scale, x, placed):
+    """A LoRA pair for ffn_gate_up: host matrices (a, b) and the device Lora.
+    placed "aligned" keeps torch's allocations; "offset" moves mid and b one
+    and three floats past 16-byte alignment."""
+    a = (rng.standard_normal((rank, k)) * 0.05).astype(np.float32)
+    b = (rng.standard_normal((n, rank)) * 0.05).astype(np.float32)
+    mid0 = ctx.lora_mid(dev(x), dev(a)) if rank else torch.zeros((m, 0), dtype=torch.float32, device="cuda")
+    if placed == "aligned":
+        return a, b, dq8.Lora(mid0, dev(b), scale)
+    mf = torch.zeros(m * rank + 1, dtype=torch.float32, device="cuda")
+    bf = torch.zeros(n * rank + 3, dtype=torch.float32, device="cuda")
+    mid, bt = mf[1:].view(m, rank), bf[3:].view(n, rank)
+    mid.copy_(mid0)
+    bt.copy_(dev(b))
+    assert mid.data_ptr() % 16 != 0 and bt.data_ptr() % 16 != 0
+    return a, b, dq8.Lora(mid, bt, scale)
+
+
+# (rows, hidden, intermediate, gate adapter, up adapter); an adapter is (rank,
+# placement) or None.  Rank 16 with aligned buffers (the reference checkpoints'
+# rank) and rank 0 run in the one-launch pair path; other ranks and offset
+# buffers go to separate gate and up launches.
+PAIR_LORA_CASES = [(130, 256, 384, (16, "aligned"), (16, "aligned")),
+                   (130, 256, 384, (16, "aligned"), None),
+                   (130, 256, 384, None, (16, "aligned")),
+                   (65, 128, 100, (16, "aligned"), (16, "aligned")),
+                   (129, 256, 72, (16, "aligned"), (0, "aligned")),
+                   (300, 1024, 520, (16, "aligned"), (16, "aligned")),
+                   (300, 1024, 520, (13, "aligned"), (16, "aligned")),
+                   (300, 1024, 520, (16, "offset"), (16, "aligned")),
+                   (1000, 2048, 2048, (16, "aligned"), (16, "aligned")),
+                   (200, 2048, 6144, (16, "aligned"), (16, "aligned"))]
+
+
+@pytest.mark.parametrize("m,hidden,inter,gl,ul", PAIR_LORA_CASES)
+def test_ffn_gate_up_with_adapters(ctx, m, hidden, inter, gl, ul):
+    # dq8_ffn_gate_up_lora: each projection's adapter term (Adapter::combine,
+    # tensor.rs:109-117, after the bias, 438) before silu(gate) * up
+    # (qwen.rs:489-490).  The same bits as the gate Write and up SwiGlu calls
+    # with their adapters and as the oracle; with quantize=True h's bytes and
+    # scales equal QuantizedInputs::new(h).
+    rng = np.random.default_rng(m * 13 + inter + hidden)
+    x = make_x(rng, m, hidden, "outliers")
+    gv, gs = dq8o.quantize_weights(make_w(rng, inter, hidden))
+    uv, us = dq8o.quantize_weights(make_w(rng, inter, hidden))
+    G, U = ctx.weights_from_quantized(dev(gv), dev(gs)), ctx.weights_from_quantized(dev(uv), dev(us))
+    q, s = ctx.quantize(dev(x))
+    gb = (rng.standard_normal(inter) * 0.5).astype(np.float32)
+    ub = (rng.standard_normal(inter) * 0.5).astype(np.float32)
+    ad = [None if spec is None else _adapter(ctx, rng, m, hidden, inter, spec[0], sc, x, spec[1])
+          for spec, sc in ((gl, 0.625), (ul, -1.5))]
+    loras = tuple(None if a is None else a[2] for a in ad)
+    got = host(ctx.ffn_gate_up(G, U, q, s, biases=(dev(gb), dev(ub)), loras=loras))
+    h = (ctx.linear_lora(G, q, s, loras[0], bias=dev(gb)) if loras[0] is not None
+         else ctx.linear(G, q, s, bias=dev(gb)))
+    if loras[1] is not None:
+        ctx.linear_lora(U, q, s, loras[1], out=h, bias=dev(ub), epilogue=dq8.SWIGLU)
+    else:
+        ctx.linear(U, q, s, out=h, bias=dev(ub), epilogue=dq8.SWIGLU)
+    assert bits_equal(got, host(h))
+    if ad[0] is not None:
+        gate = dq8o.linear_lora(x, gv, gs, ad[0][0], ad[0][1], 0.625, bias=gb, threads=8)
+    else:
+        gate = dq8o.linear(x, gv, gs, bias=gb, threads=8)
+    if ad[1] is not None:
+        want_h = dq8o.linear_lora(x, uv, us, ad[1][0], ad[1][1], -1.5, bias=ub, result=gate, epilogue=2, threads=8)
+    else:
+        want_h = dq8o.linear(x, uv, us, bias=ub, result=gate, epilogue=2, threads=8)
+    assert bits_equal(got, want_h)
+    hf, hq, hs = ctx.ffn_gate_up(G, U, q, s, biases=(dev(gb), dev(ub)), quantize=True, loras=loras)
+    assert bits_equal(host(hf), want_h)
+    oq, os_ = dq8o.quantize_inputs(want_h, threads=8)
+    assert np.array_equal(host(hq), oq) and bits_equal(host(hs), os_)
+
+
 # 65-512 rows whose wide launch would be small run as 32-row chunks on the
 # skinny kernel (dq8_linear and grouped calls through run_linear, dq8_apply
 # through its own launch); shapes on both sides of the rule's limits.
