@@ -129,6 +129,8 @@ def main():
     stream = torch.cuda.Stream(dev)
     torch.cuda.set_stream(stream)
     sh = stream.cuda_stream
+    # a second stream (default priority) for the LoRA leg's middle products that run beside a quantize
+    stream2 = torch.cuda.Stream(dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(5)
     if args.only == "skinny":
@@ -199,19 +201,45 @@ def main():
             L[key] = (a, b)
         return L[key]
 
-    def mid_call(x, a, mid, k):
-        return ("mid", lib.dq8_lora_mid, (ctx.handle, x.data_ptr(), M, k, a.data_ptr(), rank, mid.data_ptr(), sh),
-                (0, 2 * M * k * rank))
+    def mid_call(x, a, mid, k, side=False):
+        return ("mid2" if side else "mid", lib.dq8_lora_mid,
+                (ctx.handle, x.data_ptr(), M, k, a.data_ptr(), rank, mid.data_ptr(),
+                 stream2.cuda_stream if side else sh), (0, 2 * M * k * rank))
 
-    def mid_batch_call(entries):
+    def mid_batch_call(entries, side=False):
         """The middle products of projections that share an input, in one dq8_lora_mid_batch call:
         entries = [(x, A, mid, k)]."""
         arr = (dq8._MidItem * len(entries))()
         for i, (x, a, mid, k) in enumerate(entries):
             arr[i] = dq8._MidItem(x.data_ptr(), M, k, a.data_ptr(), rank, mid.data_ptr())
         keep.append(arr)
-        return ("mid", lib.dq8_lora_mid_batch, (ctx.handle, arr, len(entries), sh),
+        return ("mid2" if side else "mid", lib.dq8_lora_mid_batch,
+                (ctx.handle, arr, len(entries), stream2.cuda_stream if side else sh),
                 (0, sum(2 * M * k * rank for _, _, _, k in entries)))
+
+    def fork():
+        """stream2 waits for everything queued on the main stream so far."""
+        ev = torch.cuda.Event()
+
+        def f():
+            ev.record(stream)
+            stream2.wait_event(ev)
+            return 0
+        return ("sync", f, (), (0, 0))
+
+    def join():
+        """The main stream waits for everything queued on stream2 so far."""
+        ev = torch.cuda.Event()
+
+        def f():
+            ev.record(stream2)
+            stream.wait_event(ev)
+            return 0
+        return ("sync", f, (), (0, 0))
+
+    def beside_quant(mid, q):
+        """A middle product of x on stream2 while the main stream quantizes x: both only read x."""
+        return [fork(), mid, q, join()]
 
     def lora_linear(L, name, x, q, s, out, ep, mid, k, with_mid=True):
         """mid = linear(x, A) then the projection with its adapter (weights.rs:492-520)."""
@@ -238,8 +266,12 @@ def main():
 
         for L in layers:
             layer_bounds.append(len(calls))
-            calls.append(quant(L["x"], qx, sx, HIDDEN))
-            if L["kind"] == "gdn":
+            if with_lora and L["kind"] == "gdn":
+                calls.extend(beside_quant(mid_call(L["x"], lora_of(L, "in")[0], mids["a"], HIDDEN, side=True),
+                                          quant(L["x"], qx, sx, HIDDEN)))
+                proj(L, "in", L["x"], qx, sx, mixer_out, dq8.WRITE, mids["a"], HIDDEN, with_mid=False)
+            elif L["kind"] == "gdn":
+                calls.append(quant(L["x"], qx, sx, HIDDEN))
                 proj(L, "in", L["x"], qx, sx, mixer_out, dq8.WRITE, mids["a"], HIDDEN)
             else:
                 items = (dq8._Item * 3)()
@@ -258,20 +290,30 @@ def main():
                     items[i] = dq8._Item(L[name].handle, qx.data_ptr(), sx.data_ptr(), M, None, outs[i].data_ptr(),
                                          dq8.ROWS, dq8.WRITE, lp)
                 keep.append(items)
-                if shared:
-                    calls.append(mid_batch_call(shared))
+                if shared:  # q, k and v share their input: one grouped launch of their middle products
+                    calls.extend(beside_quant(mid_batch_call(shared, side=True), quant(L["x"], qx, sx, HIDDEN)))
+                else:
+                    calls.append(quant(L["x"], qx, sx, HIDDEN))
                 flops = sum(2 * M * L[n].n * L[n].k for n in ("q", "k", "v"))
                 calls.append(("linear", lib.dq8_linear_batch, (ctx.handle, items, 3, sh), (0, flops)))
-            calls.append(quant(L["mix"], qx, sx, HIDDEN))
-            proj(L, "out" if L["kind"] == "gdn" else "o", L["mix"], qx, sx, proj_out, dq8.WRITE, mids["a"], HIDDEN)
-            calls.append(quant(L["ffn"], qx, sx, HIDDEN))
+            mixer = "out" if L["kind"] == "gdn" else "o"
+            if with_lora:
+                calls.extend(beside_quant(mid_call(L["mix"], lora_of(L, mixer)[0], mids["a"], HIDDEN, side=True),
+                                          quant(L["mix"], qx, sx, HIDDEN)))
+            else:
+                calls.append(quant(L["mix"], qx, sx, HIDDEN))
+            proj(L, mixer, L["mix"], qx, sx, proj_out, dq8.WRITE, mids["a"], HIDDEN, with_mid=False)
             # gate and up in one launch storing h and its quantization for down (qwen.rs:489-491),
             # each with its adapter when the leg has them, then down Add
             ops = sum(2 * M * L[n].n * L[n].k for n in ("gate", "up"))
             lg = lu = None
-            if with_lora:  # gate and up share their input: one grouped launch of their middle products
-                calls.append(mid_batch_call([(L["ffn"], lora_of(L, "gate")[0], mids["b"], HIDDEN),
-                                             (L["ffn"], lora_of(L, "up")[0], mids["c"], HIDDEN)]))
+            if not with_lora:
+                calls.append(quant(L["ffn"], qx, sx, HIDDEN))
+            else:  # gate and up share their input: one grouped launch of their middle products
+                calls.extend(beside_quant(mid_batch_call([(L["ffn"], lora_of(L, "gate")[0], mids["b"], HIDDEN),
+                                                          (L["ffn"], lora_of(L, "up")[0], mids["c"], HIDDEN)],
+                                                         side=True),
+                                          quant(L["ffn"], qx, sx, HIDDEN)))
                 lg = dq8._Lora(mids["b"].data_ptr(), lora_of(L, "gate")[1].data_ptr(), rank, 2.0)
                 lu = dq8._Lora(mids["c"].data_ptr(), lora_of(L, "up")[1].data_ptr(), rank, 2.0)
                 keep.extend((lg, lu))
@@ -290,13 +332,14 @@ def main():
 
     def run_step(events=None, calls=calls):
         for i, (kind, fn, a, _) in enumerate(calls):
+            on = stream2 if kind == "mid2" else stream
             if events is not None:
-                events[i][0].record(stream)
+                events[i][0].record(on)
             st = fn(*a)
             if st != 0:
                 raise dq8.Dq8Error(st, fn.__name__)
             if events is not None:
-                events[i][1].record(stream)
+                events[i][1].record(on)
 
     for _ in range(args.warmup):
         run_step()
@@ -513,7 +556,7 @@ def run_lora_stack(args, torch, stream, build, run_step, step_ops, base_ms):
         run_step(ev[s], calls=calls)
     torch.cuda.synchronize()
     mid_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(ev_steps)
-                 for i, c in enumerate(calls) if c[0] == "mid") / ev_steps
+                 for i, c in enumerate(calls) if c[0] in ("mid", "mid2")) / ev_steps
     lin_ms = sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(ev_steps)
                  for i, c in enumerate(calls) if c[0] == "linear") / ev_steps
     return {

@@ -1868,6 +1868,9 @@ constexpr int kMidRows = 8, kMidJ = 16, kMidKT = 256, kMidStride = kMidKT + 8;
 #ifndef DQ8_MID_BATCH
 #define DQ8_MID_BATCH 8
 #endif
+#ifndef DQ8_MID_PIPE
+#define DQ8_MID_PIPE 1
+#endif
 #ifndef DQ8_MID_SMALL_M
 #define DQ8_MID_SMALL_M 32  // rows up to which k_lora_mid_small runs (0: never)
 #endif
@@ -1917,6 +1920,39 @@ __device__ __forceinline__ void lora_mid_tiled(const float* __restrict__ x, int 
     const float* as = lds[t % kMidSlots][kMidRows + jl] + i;
     const int cmax = min(kMidKT / 8, chunks - t * (kMidKT / 8));
     if (cmax == kMidKT / 8) {
+#if DQ8_MID_PIPE
+      // a full tile in batches of kMidBatch chunks, software-pipelined in three
+      // stages: the LDS operands of batch bt+2 are read while the products of
+      // batch bt+1 are formed and batch bt is added (one wave per SIMD: nothing
+      // else hides an LDS read or an MFMA issued just before its use)
+      constexpr int NB = kMidKT / 8 / kMidBatch;
+      float xo[2][kMidBatch], ao[2][kMidBatch];
+      f32x4 d[2][kMidBatch];
+      auto operands = [&](float(&xv)[kMidBatch], float(&av)[kMidBatch], int c0) {
+#pragma unroll
+        for (int u = 0; u < kMidBatch; ++u) {
+          xv[u] = xs[8 * (c0 + u)];
+          av[u] = as[8 * (c0 + u)];
+        }
+      };
+      auto products = [&](f32x4(&o)[kMidBatch], const float(&xv)[kMidBatch], const float(&av)[kMidBatch]) {
+#pragma unroll
+        for (int u = 0; u < kMidBatch; ++u) o[u] = __builtin_amdgcn_mfma_f32_4x4x1f32(xv[u], av[u], zero, 0, 0, 0);
+      };
+      operands(xo[0], ao[0], 0);
+      if (NB > 1) operands(xo[1], ao[1], kMidBatch);
+      products(d[0], xo[0], ao[0]);
+#pragma unroll
+      for (int bt = 0; bt < NB; ++bt) {
+        if (bt + 2 < NB) operands(xo[bt & 1], ao[bt & 1], kMidBatch * (bt + 2));
+        __builtin_amdgcn_sched_barrier(0);
+        if (bt + 1 < NB) products(d[(bt + 1) & 1], xo[(bt + 1) & 1], ao[(bt + 1) & 1]);
+#pragma unroll
+        for (int u = 0; u < kMidBatch; ++u)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[r] = acc[r] + d[bt & 1][u][r];
+      }
+#else
       // a full tile in batches of kMidBatch chunks: the products of the next
       // batch are formed while the current batch is added
       constexpr int NB = kMidKT / 8 / kMidBatch;
@@ -1940,6 +1976,7 @@ __device__ __forceinline__ void lora_mid_tiled(const float* __restrict__ x, int 
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[r] = acc[r] + d[bt & 1][u][r];
       }
+#endif
     } else {
       for (int c = 0; c < cmax; ++c) {
         const f32x4 d = __builtin_amdgcn_mfma_f32_4x4x1f32(xs[8 * c], as[8 * c], zero, 0, 0, 0);
