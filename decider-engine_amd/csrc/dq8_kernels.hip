@@ -398,6 +398,19 @@ __device__ __forceinline__ float max_row16(float m) {
 __device__ __forceinline__ float quant_scale(float m) {
   return (m == 0.0f) ? 1.0f : fmaxf(m / 127.0f, FLT_MIN);
 }
+// The same scale with fewer instructions: for m in [2^-100, FLT_MAX] the IEEE
+// quotient m / 127 is q0 + r * c rounded once, with c = 1/127 rounded, q0 = m *
+// c rounded and r = m - 127 * q0 exact (one FMA); the quotient is then above
+// FLT_MIN.  That equals m / 127 for every float in the range (checked
+// exhaustively on the CPU by tests/test_scale_division.py).  Other m divide.
+__device__ __forceinline__ float quant_scale_fma(float m) {
+  constexpr float c = 1.0f / 127.0f;
+  if (m >= 0x1p-100f && m <= FLT_MAX) {
+    const float q0 = m * c;
+    return __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, m), c, q0);
+  }
+  return quant_scale(m);
+}
 // N elements of one group: round(v / scale) half away from zero (f32::round of
 // the IEEE quotient), as int8 in [-127, 127], packed 4 bytes to a word.
 // The quotient is taken through rs = rcp(scale) (1 ulp): a = v * rs differs from
@@ -407,14 +420,16 @@ __device__ __forceinline__ float quant_scale(float m) {
 // (|a| < 127.0001, no clamp needed), converted and packed by v_cvt_pk_u8_f32;
 // the XOR with 0x80 turns it into the two's complement byte.  A lane with an
 // element closer than that (about 1 in 8000 elements) divides all N exactly.
-template <int N>
+// FMA: u = v * rs + 128 rounded once instead of twice; u is then within 2^-16
+// + 2^-17 of Q + 128, inside the same margin.
+template <int N, bool FMA = false>
 __device__ __forceinline__ void quant_pack(const float (&v)[N], float scale, uint32_t (&w)[N / 4]) {
   const float rs = __builtin_amdgcn_rcpf(scale);
   float r[N];
   float fm = 0.0f;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const float u = v[i] * rs + 128.0f;
+    const float u = FMA ? __builtin_fmaf(v[i], rs, 128.0f) : v[i] * rs + 128.0f;
     r[i] = rintf(u);
     fm = fmaxf(fm, fabsf(u - r[i]));
   }
@@ -526,6 +541,111 @@ __global__ __launch_bounds__(64 * DQ8_QUANT_WPB) void k_quantize(const void* __r
       }
     }
     bad = finish(v, std::false_type{});
+  }
+  if (nonfinite) {  // one atomic per wave that saw a non-finite element
+    const unsigned long long b = __ballot(bad);
+    if (b != 0 && lane == __builtin_ffsll((long long)b) - 1) atomicOr(nonfinite, 1u);
+  }
+}
+
+// The fp32 quantizer for rows of whole chunks (k % 256 == 0, 16-byte aligned x,
+// 4-byte aligned q rows): the same bytes and scales as k_quantize, from a grid
+// of at most kQuantLoopBlocks blocks whose waves walk the chunks (global chunk
+// c = row * (k / 256) + chunk of the row; wave w takes w, w + W, w + 2W, ...
+// for W waves) with D loads in flight: a chunk's slot is reloaded before the
+// chunk is finished.  Fewer, longer-lived waves keep more bytes in flight per wave than
+// one chunk per wave (2048 x 2048 fp32: a copy of the same bytes takes 4.8
+// against 5.3 us per call at one 1 KB load per wave, graph-replayed).
+#ifndef DQ8_QUANT_LOOP_BLOCKS
+#define DQ8_QUANT_LOOP_BLOCKS 1536
+#endif
+constexpr int kQuantLoopBlocks = DQ8_QUANT_LOOP_BLOCKS;
+#ifndef DQ8_QUANT_LOOP_NT_SCALES
+#define DQ8_QUANT_LOOP_NT_SCALES 1
+#endif
+#ifndef DQ8_QUANT_LOOP_BITS
+#define DQ8_QUANT_LOOP_BITS 1
+#endif
+#ifndef DQ8_QUANT_LOOP_FMA
+#define DQ8_QUANT_LOOP_FMA 1
+#endif
+#ifndef DQ8_QUANT_LOOP
+#define DQ8_QUANT_LOOP 2  // chunks in flight per wave (0: one chunk per wave, k_quantize)
+#endif
+#ifndef DQ8_QUANT_LOOP_WPB
+#define DQ8_QUANT_LOOP_WPB 4
+#endif
+template <int D>
+__global__ __launch_bounds__(64 * DQ8_QUANT_LOOP_WPB) void k_quantize_loop(const float* __restrict__ x, int k, int total,
+                                                       int8_t* __restrict__ q, int ldq, float* __restrict__ scales,
+                                                       int lds, uint32_t* nonfinite, Divider cdiv) {
+  const int lane = threadIdx.x & 63;
+  const int W = (int)gridDim.x * DQ8_QUANT_LOOP_WPB;
+  const int w = (int)blockIdx.x * DQ8_QUANT_LOOP_WPB + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int cpr = k >> 8;
+  auto load = [&](int c, float (&v)[4]) {
+    const int row = cdiv.div((uint32_t)c);
+    decode4<kDtypeF32>(x, (size_t)row * k + (size_t)(c - row * cpr) * 256 + lane * 4, v);
+  };
+  float v[D][4];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (w + d * W < total) load(w + d * W, v[d]);  // wave-uniform
+  bool bad = false;
+  for (int c0 = w; c0 < total; c0 += D * W) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int c = c0 + d * W;
+      if (c >= total) break;  // wave-uniform
+      const int row = cdiv.div((uint32_t)c), chunk = c - row * cpr;
+      float e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) e[i] = v[d][i];
+      // the slot's next load goes out before this chunk is finished (the empty
+      // asm keeps it there)
+      const int cn = c + D * W;
+      if (cn < total) load(cn, v[d]);  // wave-uniform
+      asm volatile("" ::: "memory");
+#if DQ8_QUANT_LOOP_BITS
+      // absmax and the finite check from the magnitudes' bit patterns: they
+      // order as the values do, and a NaN or an infinity has the largest
+      // exponent.  A NaN (only with the non-finite flag set, when the bytes are
+      // not used) then makes the scale NaN, where fmaxf would skip it.
+      uint32_t mb = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mb = max(mb, __builtin_bit_cast(uint32_t, e[i]) & 0x7fffffffu);
+      bad |= mb >= 0x7f800000u;
+      const float m = max_row16(__builtin_bit_cast(float, mb));
+#else
+      float m = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        bad |= !isfinite(e[i]);
+        m = fmaxf(m, fabsf(e[i]));
+      }
+      m = max_row16(m);  // over the 16 lanes of this group
+#endif
+#if DQ8_QUANT_LOOP_FMA
+      const float scale = quant_scale_fma(m);
+      uint32_t pk[1];
+      quant_pack<4, true>(e, scale, pk);
+#else
+      const float scale = quant_scale(m);
+      uint32_t pk[1];
+      quant_pack<4>(e, scale, pk);
+#endif
+#if DQ8_QUANT_NTS
+      __builtin_nontemporal_store(pk[0], reinterpret_cast<uint32_t*>(q + (size_t)row * ldq + chunk * 256 + lane * 4));
+#if DQ8_QUANT_LOOP_NT_SCALES
+      if ((lane & 15) == 0) __builtin_nontemporal_store(scale, scales + (size_t)row * lds + chunk * 4 + (lane >> 4));
+#else
+      if ((lane & 15) == 0) scales[(size_t)row * lds + chunk * 4 + (lane >> 4)] = scale;
+#endif
+#else
+      *reinterpret_cast<uint32_t*>(q + (size_t)row * ldq + chunk * 256 + lane * 4) = pk[0];
+      if ((lane & 15) == 0) scales[(size_t)row * lds + chunk * 4 + (lane >> 4)] = scale;
+#endif
+    }
   }
   if (nonfinite) {  // one atomic per wave that saw a non-finite element
     const unsigned long long b = __ballot(bad);
@@ -2279,6 +2399,18 @@ hipError_t launch_lora_mid(const float* x, int m, int k, const float* a, int ran
 
 hipError_t launch_quantize_raw(const void* x, int dtype, int rows, int k, int8_t* q, int ldq, float* scales, int lds,
                                uint32_t* nonfinite, hipStream_t s) {
+#if DQ8_QUANT_LOOP > 0
+  if (dtype == kDtypeF32 && k % 256 == 0 && ((uintptr_t)x & 15) == 0 && ldq % 4 == 0 && ((uintptr_t)q & 3) == 0) {
+    const long total = (long)rows * (k / 256);
+    if (total == 0) return hipSuccess;
+    if (total < (1L << 31) - 4L * kQuantLoopBlocks) {
+      const int blocks = (int)std::min<long>(kQuantLoopBlocks, (total + DQ8_QUANT_LOOP_WPB - 1) / DQ8_QUANT_LOOP_WPB);
+      k_quantize_loop<DQ8_QUANT_LOOP><<<blocks, 64 * DQ8_QUANT_LOOP_WPB, 0, s>>>(static_cast<const float*>(x), k, (int)total, q, ldq,
+                                                             scales, lds, nonfinite, Divider::of((uint32_t)(k / 256)));
+      return hipGetLastError();
+    }
+  }
+#endif
   constexpr int PER = DQ8_QUANT_PER;
   const long waves = (long)rows * (((k + 255) / 256 + PER - 1) / PER);
   if (waves == 0) return hipSuccess;

@@ -79,6 +79,32 @@ def test_quantize_bit_exact(ctx, rows, width, kind):
     assert bits_equal(host(s), want_s)
 
 
+# Widths that are a multiple of 256 run on the chunk-walking quantizer: the
+# sizes below give its waves one chunk, and several with a ragged last round.
+@pytest.mark.parametrize("rows,width", [(2048, 2048), (1543, 2304), (5, 512)])
+@pytest.mark.parametrize("kind", ["normal", "edge", "student"])
+def test_quantize_chunk_walk_bit_exact(ctx, rows, width, kind):
+    rng = np.random.default_rng(rows + width * 3)
+    x = make_x(rng, rows, width, kind)
+    q, s = ctx.quantize(dev(x))
+    want_q, want_s = dq8o.quantize_inputs(x, threads=8)
+    assert np.array_equal(host(q), want_q)
+    assert bits_equal(host(s), want_s)
+
+
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+@pytest.mark.parametrize("where", [(0, 0), (2, 511), (1537, 100)])
+def test_quantize_chunk_walk_reports_nonfinite(ctx, bad, where):
+    rows = 1600 if where[0] >= 3 else 3
+    x = np.ones((rows, 512), np.float32)
+    x[where] = bad
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ctx.quantize(dev(x), nonfinite=flag)
+    assert int(host(flag)[0]) == 1
+    with pytest.raises(dq8.NonFinite):
+        ctx.quantize(dev(x))
+
+
 def test_quantize_values_next_to_half_integer_boundaries(ctx):
     # Every element of a group is (k + 0.5) * scale, rounded, and moved by up
     # to 2 ulp either way, for random k in -127..126: the quotient by the scale

@@ -43,6 +43,19 @@ def shortcut(v, s, du, margin):
     return fast, r.astype(np.float64) - 128.0
 
 
+def shortcut_fma(v, s, du, margin):
+    # u = v * rs + 128 rounded once (an FMA): the product is exact in the
+    # x87 extended format (48 significant bits), and so is the sum whenever
+    # |v * rs| >= 2^-10 (64 bits); smaller products leave u within 2^-9 of
+    # 128, where a second rounding cannot change rint(u) or the margin test.
+    rs = ((F32(1.0) / s).astype(F32).view(np.int32) + du).view(F32)
+    u = (v.astype(np.longdouble) * rs.astype(np.longdouble) + np.longdouble(128.0)).astype(F32)
+    r = np.rint(u).astype(F32)
+    f = (u - r).astype(F32)
+    fast = (F32(0.5) - np.abs(f)).astype(F32) > margin
+    return fast, r.astype(np.float64) - 128.0
+
+
 def test_shortcut_agrees_with_the_ieee_quotient_next_to_boundaries():
     rng = np.random.default_rng(1)
     taken = 0
@@ -51,10 +64,11 @@ def test_shortcut_agrees_with_the_ieee_quotient_next_to_boundaries():
         want = round_half_away((v / s).astype(F32).astype(np.float64))
         assert np.abs(want).max() <= 127
         for du in (-1, 0, 1):  # any reciprocal within 1 ulp
-            fast, got = shortcut(v, s, du, MARGIN)
-            assert np.array_equal(got[fast], want[fast])
-            assert np.abs(got[fast]).max() <= 127
-            taken += int(fast.sum())
+            for form in (shortcut, shortcut_fma):  # u from a multiply and an add, or one FMA
+                fast, got = form(v, s, du, MARGIN)
+                assert np.array_equal(got[fast], want[fast])
+                assert np.abs(got[fast]).max() <= 127
+                taken += int(fast.sum())
     assert taken > 0
 
 
