@@ -811,6 +811,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 #ifndef DQ8_WIDE_WPE
 #define DQ8_WIDE_WPE 0
 #endif
+// > 0: the wide kernel runs as a grid of at most DQ8_WIDE_PERSIST blocks per CU
+// (256 CUs) that walk the tiles; 0: one block per tile.
+#ifndef DQ8_WIDE_PERSIST
+#define DQ8_WIDE_PERSIST 0
+#endif
 // 256-element chunks per wave of the quantizer.
 #ifndef DQ8_QUANT_PER
 #define DQ8_QUANT_PER 1
@@ -922,9 +927,13 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   __shared__ __attribute__((aligned(16))) XChunk xc[DOTS ? 1 : 2];
   if (b.unless && *b.unless) return;  // non-finite inputs: the FP32 kernel runs instead
 
-  const int lane = threadIdx.x & 63;
+  // One tile (block index blk of the launch's tile list).
+  auto run_tile = [&](const int blk) {
+  // the lane id through an empty volatile asm: everything derived from it is
+  // recomputed per tile instead of being held in registers across the tiles
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int blk = blockIdx.x;
   const int pidx = find_proj(b, blk);
   const Proj P = b.p[pidx];
   int mt, nt;
@@ -1397,6 +1406,19 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       }
     store_tile(P, rows, cols, y);
   }
+  };
+#if DQ8_WIDE_PERSIST > 0
+  // A grid of resident blocks walks the tile list: block i takes tiles i, i +
+  // gridDim.x, ...  (gridDim.x a multiple of 8 keeps each tile on the XCD the
+  // plain launch would give it).  The barrier keeps the next tile's loads out
+  // of LDS the previous epilogue may still read.
+  for (int t = blockIdx.x; t < b.total_waves; t += gridDim.x) {
+    run_tile(t);
+    __syncthreads();
+  }
+#else
+  run_tile(blockIdx.x);
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -2506,15 +2528,20 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
     for (int i = 0; i < b.count; ++i) (b.p[i].g > 32 ? has_long : has_short) = true;
     const bool deep = b.total_waves <= DQ8_WIDE_DEEP_BLOCKS ||
                       (has_long && has_short && b.total_waves <= DQ8_WIDE_DEEP_MIXED);
+#if DQ8_WIDE_PERSIST > 0
+    const int grid = std::min(b.total_waves, DQ8_WIDE_PERSIST * 256);
+#else
+    const int grid = b.total_waves;
+#endif
 #define DQ8_WIDE(SA, SB, X, D, L)                                                                \
   k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, SA, SB, X, DQ8_WIDE_SWZ, D, L> \
-      <<<b.total_waves, threads, 0, s>>>(b)
+      <<<grid, threads, 0, s>>>(b)
     constexpr int S0 = DQ8_WIDE_STAGES, S1 = DQ8_WIDE_STAGES + 1, X = DQ8_WIDE_XCH;
     bool pair_lora = false;
     for (int i = 0; i < b.count; ++i) pair_lora |= b.p[i].pair && (b.p[i].lora || b.p[i].lora2);
     if (pair_lora) {  // a SwiGLU pair with adapters
       k_linear_wide<DQ8_WIDE_WM, DQ8_WIDE_WN, DQ8_WIDE_RT, DQ8_WIDE_CT, 2, 3, 8, DQ8_WIDE_SWZ, false, true, true>
-          <<<b.total_waves, threads, 0, s>>>(b);
+          <<<grid, threads, 0, s>>>(b);
       return hipGetLastError();
     }
     if (dots) DQ8_WIDE(S0, S0, X, true, false);
