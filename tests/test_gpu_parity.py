@@ -1079,6 +1079,38 @@ PAIR_LORA_CASES = [(130, 256, 384, (16, "aligned"), (16, "aligned")),
                    (200, 2048, 6144, (16, "aligned"), (16, "aligned"))]
 
 
+def test_ffn_gate_up_with_adapters_full_size(ctx):
+    # The 2048-token stack's FFN shape (2048 x 2048 -> 2 x 6144, rank-16
+    # adapters on gate and up, biases, h quantized in the launch): the pair
+    # launch equals the separate gate Write and up SwiGlu launches with their
+    # adapters on every output, and the oracle on one row of every 64-row tile.
+    m, hidden, inter, rank = 2048, 2048, 6144, 16
+    rng = np.random.default_rng(2049)
+    x = make_x(rng, m, hidden, "student")
+    gv, gs = dq8o.quantize_weights(make_w(rng, inter, hidden))
+    uv, us = dq8o.quantize_weights(make_w(rng, inter, hidden))
+    G, U = ctx.weights_from_quantized(dev(gv), dev(gs)), ctx.weights_from_quantized(dev(uv), dev(us))
+    q, s = ctx.quantize(dev(x))
+    gb = (rng.standard_normal(inter) * 0.5).astype(np.float32)
+    ub = (rng.standard_normal(inter) * 0.5).astype(np.float32)
+    ga, gbm = (rng.standard_normal((rank, hidden)) * 0.05).astype(np.float32), \
+        (rng.standard_normal((inter, rank)) * 0.05).astype(np.float32)
+    ua, ubm = (rng.standard_normal((rank, hidden)) * 0.05).astype(np.float32), \
+        (rng.standard_normal((inter, rank)) * 0.05).astype(np.float32)
+    gl = dq8.Lora(ctx.lora_mid(dev(x), dev(ga)), dev(gbm), 0.625)
+    ul = dq8.Lora(ctx.lora_mid(dev(x), dev(ua)), dev(ubm), -1.5)
+    h, hq, hs = ctx.ffn_gate_up(G, U, q, s, biases=(dev(gb), dev(ub)), quantize=True, loras=(gl, ul))
+    sep = ctx.linear_lora(G, q, s, gl, bias=dev(gb))
+    ctx.linear_lora(U, q, s, ul, out=sep, bias=dev(ub), epilogue=dq8.SWIGLU)
+    assert bits_equal(host(h), host(sep))
+    rq, rs = ctx.quantize(sep)
+    assert np.array_equal(host(hq), host(rq)) and bits_equal(host(hs), host(rs))
+    rows = tile_rows(rng, m)
+    gate = dq8o.linear_lora(x[rows], gv, gs, ga, gbm, 0.625, bias=gb, threads=8)
+    want = dq8o.linear_lora(x[rows], uv, us, ua, ubm, -1.5, bias=ub, result=gate, epilogue=2, threads=8)
+    assert bits_equal(host(h)[rows], want)
+
+
 @pytest.mark.parametrize("m,hidden,inter,gl,ul", PAIR_LORA_CASES)
 def test_ffn_gate_up_with_adapters(ctx, m, hidden, inter, gl, ul):
     # dq8_ffn_gate_up_lora: each projection's adapter term (Adapter::combine,
