@@ -2425,7 +2425,8 @@ hipError_t launch_quantize_raw(const void* x, int dtype, int rows, int k, int8_t
   if (dtype == kDtypeF32 && k % 256 == 0 && ((uintptr_t)x & 15) == 0 && ldq % 4 == 0 && ((uintptr_t)q & 3) == 0) {
     const long total = (long)rows * (k / 256);
     if (total == 0) return hipSuccess;
-    if (total < (1L << 31) - 4L * kQuantLoopBlocks) {
+    // the waves' chunk indices run to total + (DQ8_QUANT_LOOP + 1) * W (W <= 4 * kQuantLoopBlocks) in int
+    if (total < (1L << 31) - (DQ8_QUANT_LOOP + 1) * (long)DQ8_QUANT_LOOP_WPB * kQuantLoopBlocks) {
       const int blocks = (int)std::min<long>(kQuantLoopBlocks, (total + DQ8_QUANT_LOOP_WPB - 1) / DQ8_QUANT_LOOP_WPB);
       k_quantize_loop<DQ8_QUANT_LOOP><<<blocks, 64 * DQ8_QUANT_LOOP_WPB, 0, s>>>(static_cast<const float*>(x), k, (int)total, q, ldq,
                                                              scales, lds, nonfinite, Divider::of((uint32_t)(k / 256)));
