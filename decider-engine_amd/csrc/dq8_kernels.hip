@@ -929,10 +929,12 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 
   // One tile (block index blk of the launch's tile list).
   auto run_tile = [&](const int blk) {
+  int lane = threadIdx.x & 63;
+#if DQ8_WIDE_PERSIST > 0
   // the lane id through an empty volatile asm: everything derived from it is
   // recomputed per tile instead of being held in registers across the tiles
-  int lane = threadIdx.x & 63;
   asm volatile("" : "+v"(lane));
+#endif
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
   const int pidx = find_proj(b, blk);
   const Proj P = b.p[pidx];
