@@ -1257,20 +1257,21 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       // block at a time: block b of pair j is row tile b (RT == 2) or column
       // tile b (RT == 1); products from a K=2 MFMA whose k=1 operands (lanes
       // 32-63) are zero.  For rank <= 16 the wave first copies its mid rows and
-      // b columns into the (now idle) LDS ring, rows padded to 17 floats so the
-      // operand reads hit distinct banks; the products then wait on LDS, not L2.
+      // b columns into the (now idle) LDS ring; the products then wait on LDS,
+      // not L2.
       v16f zero16;
 #pragma unroll
       for (int i = 0; i < 16; ++i) zero16[i] = 0.0f;
       const bool k0 = lane < 32;
-      // Operand rows of 16 floats, element i of row r at r*16 + (i ^ ((r >> 2) & 15)):
-      // the 32 lanes reading one element of 32 consecutive rows hit 32 banks.
-      constexpr int WROWS = 32 * RT, WCOLS = 32 * CT, LWAVE = (WROWS + WCOLS) * 16 * 4;
+      // Operand rows padded to kLoraRow = 17 floats: the 32 lanes reading one
+      // element of 32 consecutive rows hit 32 banks, and every operand read is
+      // a base register plus an immediate offset (no address arithmetic).
+      constexpr int WROWS = 32 * RT, WCOLS = 32 * CT, LWAVE = (WROWS + WCOLS) * kLoraRow * 4;
       constexpr bool FITS = NW * LWAVE <= (int)sizeof(Ring);
       const bool staged = FITS && P.rank <= 16;
       float* lmid = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(&ring) + wid * LWAVE);
-      float* lbw = lmid + WROWS * 16;
-      auto sw = [](int r, int i) { return r * 16 + (i ^ ((r >> 2) & 15)); };
+      float* lbw = lmid + WROWS * kLoraRow;
+      auto sw = [](int r, int i) { return r * kLoraRow + i; };
       if (staged) {
         lds_barrier();  // every wave is done reading the ring
         // The wave's mid rows mw.. and b rows nw.. are contiguous runs of
@@ -1351,21 +1352,15 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
             // v_mfma_f32_4x4x1_16b_f32 forms a slice's products for one index,
             // A lane l = mid[row 8u + 4(l/32) + l%4], B lane l = b[col l%32],
             // so every slice sums on its own in 4 registers.
-            const float* rm[4];
-            int xm[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int ar = (RT == 2 ? 32 * bk : 0) + 8 * u + 4 * (lane >> 5) + (lane & 3);
-              rm[u] = lmid + 16 * ar;
-              xm[u] = (ar >> 2) & 15;
-            }
-            const float* rb = lbw + 16 * c;
-            const int xb = (c >> 2) & 15;
+            // row 8u + 4(l/32) + l%4 of slice u sits 8u rows past slice 0's
+            const float* rm0 = lmid + kLoraRow * ((RT == 2 ? 32 * bk : 0) + 4 * (lane >> 5) + (lane & 3));
+            const float* rb = lbw + kLoraRow * c;
             const v4f zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
             v16f sum;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-              auto prod = [&](int i) { return mfma_k1_4(rm[u][i ^ xm[u]], rb[i ^ xb], zero4); };
+              const float* rmu = rm0 + 8 * kLoraRow * u;
+              auto prod = [&](int i) { return mfma_k1_4(rmu[i], rb[i], zero4); };
               v4f su;
               if (P.rank == 16) {
 #pragma unroll
