@@ -704,6 +704,35 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
     # questions); the eager rate above is reported beside it
     lora = run_skinny_lora(args, torch, dq8, ctx, lib, dev, stream, gen, shapes, copies, acts, launches)
     graph_q_ms = lora["plain_ms_per_question"]
+    # two questions in flight: the questions are independent (each continues from the shared prefix), so the
+    # graph alternates their launches over two streams; one launch's ramp and tail overlap the other's stream
+    side = torch.cuda.Stream(dev)
+
+    def go_two():
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        side.wait_event(ev)
+        for qi, items in enumerate(launches):
+            st = lib.dq8_linear_batch(ctx.handle, items, len(shapes), (side if qi % 2 else stream).cuda_stream)
+            if st != 0:
+                raise dq8.Dq8Error(st, "dq8_linear_batch")
+        back = torch.cuda.Event()
+        back.record(side)
+        stream.wait_event(back)
+
+    go_two()
+    torch.cuda.synchronize()
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2, stream=stream):
+        go_two()
+    g2.replay()
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(reps):
+        g2.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    two_q_ms = t0.elapsed_time(t1) / (reps * args.questions)
     # the same projections as a model issues them, one launch per input: x (q, k, v, GDN in), the mixer outputs
     # (o, GDN out), the FFN input (gate, up), h (down); graph-replayed like the grouped launch
     parts = [[0, 1, 2, 4], [3, 5], [6, 7], [8]]
@@ -759,6 +788,13 @@ def run_skinny(args, torch, dq8, ctx, lib, dev, stream, gen):
             "traffic": load_traffic("linear_skinny_questions24"),
             "bytes_per_launch": wbytes,
             "avg_launch_ms": round(avg_launch, 5),
+        },
+        "two_in_flight": {
+            "workload": "the same question launches alternating over two streams of one HIP graph (two questions "
+                        "in flight; the 5 rotating weight copies keep their bytes distinct)",
+            "ms_per_question": round(two_q_ms, 5),
+            "gbs": round(wbytes / (two_q_ms * 1e-3) / 1e9, 1),
+            "frac": round(wbytes / (two_q_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
         },
         "layer_order_launches": {
             "workload": "the same questions, each as 4 launches in a layer's order: q,k,v + GDN in (x), o + GDN out "

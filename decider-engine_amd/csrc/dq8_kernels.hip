@@ -1441,10 +1441,9 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 //    NSEG rings in flight.  A block covers one 16-row tile of its strip (17-32
 //    rows: two blocks per strip, so each weight byte is read twice, the second
 //    time mostly from cache), so a ring step is one activation and one weight
-//    fragment and the ring can run
-//    8 steps ahead (the load latency under a full stream is microseconds;
-//    both row tiles in one block held the ring to 6 steps at 210 VGPRs, and
-//    deeper went past 256).  Activation fragments join the register ring;
+//    fragment and the ring runs 6 steps ahead (the load latency under a full
+//    stream is microseconds; 8 steps measured 1-2% slower for a 24-row layer
+//    set at 180 against 144 VGPRs).  Activation fragments join the register ring;
 //    x scales come through LDS in chunks of 8 steps.  Per step every wave
 //    posts its t's to LDS and, after a barrier, the strip's first wave adds
 //    them in group order: every output is still one left-to-right sum.
@@ -2481,7 +2480,8 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
 }
 
 // Skinny launch shape (tunable at build time): a short-K wave covers 16*CT
-// columns, a long-K wave 16*CTL; DBS / DBL steps in flight in their rings.
+// columns, a long-K wave 16*CTL; DBS / DBL steps in flight in their rings
+// (DBS2 / DBL2 in the 17-32 row kernel).
 #ifndef DQ8_SKINNY_CT
 #define DQ8_SKINNY_CT 2
 #endif
@@ -2494,8 +2494,11 @@ hipError_t launch_pad_rows(const int8_t* q, int rows, int k, int8_t* dst, int ld
 #ifndef DQ8_SKINNY_DBL
 #define DQ8_SKINNY_DBL 6
 #endif
+#ifndef DQ8_SKINNY_DBS2
+#define DQ8_SKINNY_DBS2 3  // the short-K ring of the 17-32 row kernel
+#endif
 #ifndef DQ8_SKINNY_DBL2
-#define DQ8_SKINNY_DBL2 8  // the long-K ring of the 17-32 row kernel
+#define DQ8_SKINNY_DBL2 6  // the long-K ring of the 17-32 row kernel
 #endif
 // Short K (G <= 32) runs one wave per strip; longer K interleaves a strip's
 // groups over 4 waves.
@@ -2557,9 +2560,10 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
     return hipGetLastError();
   }
   // total_waves counts blocks of 4 waves for the skinny kernel; kind 1: M <= 16, kind 2: M <= 32
-  constexpr int CT = DQ8_SKINNY_CT, CL = DQ8_SKINNY_CTL, DS = DQ8_SKINNY_DBS, DL = DQ8_SKINNY_DBL;
-#define DQ8_SKINNY(R, D, L) \
-  k_linear_skinny<R, CT, CL, DS, (R == 1 ? DL : DQ8_SKINNY_DBL2), D, L><<<b.total_waves, 256, 0, s>>>(b)
+  constexpr int CT = DQ8_SKINNY_CT, CL = DQ8_SKINNY_CTL;
+#define DQ8_SKINNY(R, D, L)                                                                                  \
+  k_linear_skinny<R, CT, CL, (R == 1 ? DQ8_SKINNY_DBS : DQ8_SKINNY_DBS2), (R == 1 ? DQ8_SKINNY_DBL : DQ8_SKINNY_DBL2), \
+                  D, L><<<b.total_waves, 256, 0, s>>>(b)
   if (kind == 1) {
     if (dots) DQ8_SKINNY(1, true, false);
     else if (lora) DQ8_SKINNY(1, false, true);
