@@ -1094,6 +1094,9 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int j = 0; j < CT; ++j) dt[r][j] = mfma_i8(af[r][0], bf[j][0], cinit);
+      // cinit stays in its 16 VGPRs: left to itself the compiler rebuilds it
+      // from SGPRs in half the groups (8 v_mov_b64 each)
+      asm volatile("" : "+v"(cinit));
 #pragma unroll
       for (int r = 0; r < RT; ++r)
 #pragma unroll
