@@ -123,16 +123,22 @@ __device__ __forceinline__ float silu(float x) {
 //    reciprocal is subnormal and y = 1 + e takes the division.
 struct ExpTab {
   int lo, hi;  // lane l holds kExp2Frac[l % 32]
+  // kShift and c1 of expf_wave: each shares an FMA with another double
+  // constant, so one of the two must sit in VGPRs; held here once rather than
+  // rebuilt by two moves per call
+  double shift, c1;
 };
 __device__ __forceinline__ ExpTab exp_table(int lane) {
   const uint64_t t = __builtin_bit_cast(uint64_t, kExp2Frac[lane & 31]);
-  return {(int)(uint32_t)t, (int)(uint32_t)(t >> 32)};
+  double shift = 0x1.8p+52, c1 = 0x1.ebfce50fac4f3p-13;
+  asm volatile("" : "+v"(shift), "+v"(c1));
+  return {(int)(uint32_t)t, (int)(uint32_t)(t >> 32), shift, c1};
 }
 __device__ __forceinline__ float expf_wave(float x, const ExpTab& T) {
   constexpr double kInvLn2x32 = 0x1.71547652b82fep+0 * 32, kShift = 0x1.8p+52;
-  constexpr double c0 = 0x1.c6af84b912394p-20, c1 = 0x1.ebfce50fac4f3p-13, c2 = 0x1.62e42ff0c52d6p-6;
+  constexpr double c0 = 0x1.c6af84b912394p-20, c2 = 0x1.62e42ff0c52d6p-6;
   const double xd = x;
-  double kd = __builtin_fma(kInvLn2x32, xd, kShift);
+  double kd = __builtin_fma(kInvLn2x32, xd, T.shift);
   const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
   kd -= kShift;
   const double r = __builtin_fma(kInvLn2x32, xd, -kd);
@@ -141,20 +147,28 @@ __device__ __forceinline__ float expf_wave(float x, const ExpTab& T) {
   const uint32_t thi = (uint32_t)__builtin_amdgcn_ds_bpermute(j << 2, T.hi);
   const uint64_t tb = ((uint64_t)thi << 32) | tlo;
   const double sc = __builtin_bit_cast(double, tb + ((ki - (uint64_t)j) << 47));
-  const double z = __builtin_fma(c0, r, c1);
+  const double z = __builtin_fma(c0, r, T.c1);
   const double r2 = r * r;
   double y = __builtin_fma(c2, r, 1.0);
   y = __builtin_fma(z, r2, y);
   float v = (float)(y * sc);
-  v = x >= 89.0f ? __builtin_inff() : v;
-  v = x <= -104.0f ? 0.0f : v;
-  return x != x ? x + x : v;
+  // The special ranges (and NaN) are rare: their selects run only when some
+  // lane of the wave needs them (a wave-uniform branch).
+  if (__ballot(!(x > -104.0f && x < 89.0f)) != 0) {
+    asm volatile("");  // keeps the compiler from evaluating the selects unconditionally
+    v = x >= 89.0f ? __builtin_inff() : v;
+    v = x <= -104.0f ? 0.0f : v;
+    v = x != x ? x + x : v;
+  }
+  return v;
 }
 __device__ __forceinline__ float silu_wave(float x, const ExpTab& T) {
   const float y = 1.0f + expf_wave(-x, T);
   const float r0 = __builtin_amdgcn_rcpf(y);
   float rq = __builtin_fmaf(__builtin_fmaf(-y, r0, 1.0f), r0, r0);
-  if (!(y <= 0x1p126f)) rq = 1.0f / y;  // subnormal reciprocal, inf or NaN
+  // subnormal reciprocal, inf or NaN: the division, only when some lane of
+  // the wave has such a y (otherwise the compiler evaluates it for every lane)
+  if (__ballot(!(y <= 0x1p126f)) != 0) rq = !(y <= 0x1p126f) ? 1.0f / y : rq;
   return x * rq;
 }
 
@@ -1179,14 +1193,29 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       }
       const ExpTab T = exp_table(lane);
       float hv[16];
+      // A wave tile inside m x n (uniform) stores with no per-value checks: a
+      // wave-uniform row base plus a fixed 32-bit lane offset per store.
+      auto h_tile = [&](auto full_tag) {
+        constexpr bool FULL = decltype(full_tag)::value;
+        const uint32_t loff = (uint32_t)((4 * (lane >> 5)) * P.n + col) * 4u;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int row = mw + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        const float yg = s[0][v], yu = s[0][16 + v];
-        hv[v] = silu_wave(yg, T) * yu;
-        if (row < P.m && col < P.n) st_out(P.out + (size_t)row * P.n + col, hv[v]);
-        if ((v & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-      }
+        for (int v = 0; v < 16; ++v) {
+          const int row = mw + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          const float yg = s[0][v], yu = s[0][16 + v];
+          hv[v] = silu_wave(yg, T) * yu;
+          if constexpr (FULL) {
+            char* rb = reinterpret_cast<char*>(P.out + (size_t)(mw + 8 * (v >> 2) + (v & 3)) * P.n);
+            st_out(reinterpret_cast<float*>(rb + loff), hv[v]);
+          } else {
+            if (row < P.m && col < P.n) st_out(P.out + (size_t)row * P.n + col, hv[v]);
+          }
+          if ((v & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      if (mw + 32 <= P.m && n0 + 64 <= P.n)
+        h_tile(std::true_type{});
+      else
+        h_tile(std::false_type{});
       if (P.hq != nullptr) {  // uniform over the launch
         // h re-quantized for the down projection (qwen.rs:491, QuantizedInputs::new,
         // tensor.rs:321-339): the block holds 64 whole groups (rows m0.., columns
