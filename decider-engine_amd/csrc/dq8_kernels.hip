@@ -226,6 +226,36 @@ __device__ __forceinline__ void store_tile(const Proj& P, const int (&row)[E], c
   }
 }
 
+// store_tile for E values of a tile inside m x n in the rows layout: value e
+// at row ur[e], column uc[e] (wave-uniform) plus the lane's fixed byte offset
+// loff, so no bounds checks and no per-value address arithmetic on the VALU.
+template <int E>
+__device__ __forceinline__ void store_tile_full(const Proj& P, const int (&ur)[E], const int (&uc)[E], uint32_t loff,
+                                                const float (&y)[E]) {
+  auto at = [&](int e) {
+    return reinterpret_cast<float*>(reinterpret_cast<char*>(P.out + (size_t)ur[e] * P.n + uc[e]) + loff);
+  };
+  if (P.epilogue == 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) st_out(at(e), y[e]);
+    return;
+  }
+  float old[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) old[e] = *at(e);
+  if (P.epilogue == 1) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) st_out(at(e), old[e] + y[e]);
+    return;
+  }
+  const ExpTab T = exp_table((int)(threadIdx.x & 63));
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    st_out(at(e), silu_wave(old[e], T) * y[e]);
+    if ((e & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 __device__ __forceinline__ int find_proj(const Batch& b, int wave) {
   int pi = 0;
   for (int i = 1; i < b.count; ++i)
@@ -1423,17 +1453,23 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
     constexpr int E = NP * 32;
     int rows[E], cols[E];
     float y[E];
+    // with the wave's tile inside m x n (uniform), rows and columns split into
+    // a wave-uniform part and the lane's fixed offset (4*(lane/32), lane%32)
+    const bool full = P.layout == 0 && mw + WR <= P.m && nw + WC <= P.n;
 #pragma unroll
     for (int j = 0; j < NP; ++j)
 #pragma unroll
       for (int v = 0; v < 32; ++v) {
         const int blk2 = v >> 4, vv = v & 15;
         const int r = RT == 2 ? blk2 : 0, c = RT == 2 ? j : blk2;
-        rows[32 * j + v] = mw + 32 * r + 8 * (vv >> 2) + 4 * (lane >> 5) + (vv & 3);
-        cols[32 * j + v] = nw + 32 * c + (lane & 31);
+        rows[32 * j + v] = mw + 32 * r + 8 * (vv >> 2) + (vv & 3) + (full ? 0 : 4 * (lane >> 5));
+        cols[32 * j + v] = nw + 32 * c + (full ? 0 : (lane & 31));
         y[32 * j + v] = s[j][v];
       }
-    store_tile(P, rows, cols, y);
+    if (full)
+      store_tile_full(P, rows, cols, (uint32_t)(4 * (lane >> 5) * P.n + (lane & 31)) * 4u, y);
+    else
+      store_tile(P, rows, cols, y);
   }
   };
 #if DQ8_WIDE_PERSIST > 0
