@@ -365,6 +365,16 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips, long lau
     const int row_tiles = (p.m + dq8::wide_block_rows() - 1) / dq8::wide_block_rows();
     p.xcd_gm = xcd_rows_split(row_tiles, p.waves_n, (size_t)p.m * p.g, (size_t)(p.pair ? 2 : 1) * p.n * p.g);
     xcd_chunks(p, row_tiles);
+    p.d_cols = dq8::Divider::of((uint32_t)std::max(1, p.waves_n));
+    if (p.xcd_gm) {
+      const int gn = 8 / p.xcd_gm;
+      p.xcd_rm = row_tiles / p.xcd_gm;
+      p.xcd_rn = p.waves_n / gn;
+      p.xcd_gn_shift = gn == 8 ? 3 : gn == 4 ? 2 : gn == 2 ? 1 : 0;
+      p.d_band = dq8::Divider::of((uint32_t)(p.xcd_sr * p.xcd_rn));
+      p.d_chunk = dq8::Divider::of((uint32_t)(p.xcd_sr * p.xcd_sc));
+      p.d_sr = dq8::Divider::of((uint32_t)p.xcd_sr);
+    }
     b.total_waves += p.waves_n * row_tiles;
   } else {
     p.nseg = dq8::skinny_segments(p.g, few_strips);

@@ -27,6 +27,21 @@ struct Weights {
   float* scales;
 };
 
+// Division by a fixed d >= 1 for 0 <= n < 2^31 without a divide (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994,
+// Thm 4.2): with l = ceil(log2 d) and mul = ceil(2^(31+l) / d) < 2^32,
+// floor(n / d) = (n * mul) >> (31 + l), since 0 <= mul*d - 2^(31+l) < d <= 2^l.
+struct Divider {
+  uint32_t mul;
+  int shift;
+  static Divider of(uint32_t d) {
+    int l = 0;
+    while ((1ull << l) < d) ++l;
+    return {(uint32_t)(((1ull << (31 + l)) + d - 1) / d), 31 + l};
+  }
+  __host__ __device__ int div(uint32_t n) const { return (int)(((uint64_t)n * mul) >> shift); }
+};
+
 // One projection of a launch.  q is [M][ldq] bytes with ldq % 16 == 0 and
 // every byte up to G*64 of each row readable (zero past K).
 struct Proj {
@@ -51,6 +66,11 @@ struct Proj {
   int units;          // skinny short K: at most this many 16-column units per block (2..8)
   int xcd_gm;         // wide: row bands of the per-XCD tile regions (1, 2, 4, 8), 0 = row-major order
   int xcd_sr, xcd_sc; // wide: a region is walked in chunks of xcd_sr row tiles x xcd_sc column tiles
+  // wide: the tile walk's divisors, set with the fields above: region size in
+  // row and column tiles, log2 of the 8 / xcd_gm column bands, and dividers by
+  // waves_n, xcd_sr * xcd_rn, xcd_sr * xcd_sc and xcd_sr
+  int xcd_rm, xcd_rn, xcd_gn_shift;
+  Divider d_cols, d_band, d_chunk, d_sr;
   int nseg;           // skinny: waves per strip (1 or 4)
   // Fused SwiGLU pair (wide kernel only): wt/wst/bias are the gate weights,
   // wt2/wst2/bias2 the up weights of the same shape; the launch stores
@@ -71,21 +91,6 @@ struct Proj {
   int lora2;
   int rank2;
   float lscale2;
-};
-
-// Division by a fixed d >= 1 for 0 <= n < 2^31 without a divide (Granlund and
-// Montgomery, "Division by invariant integers using multiplication", 1994,
-// Thm 4.2): with l = ceil(log2 d) and mul = ceil(2^(31+l) / d) < 2^32,
-// floor(n / d) = (n * mul) >> (31 + l), since 0 <= mul*d - 2^(31+l) < d <= 2^l.
-struct Divider {
-  uint32_t mul;
-  int shift;
-  static Divider of(uint32_t d) {
-    int l = 0;
-    while ((1ull << l) < d) ++l;
-    return {(uint32_t)(((1ull << (31 + l)) + d - 1) / d), 31 + l};
-  }
-  __host__ __device__ int div(uint32_t n) const { return (int)(((uint64_t)n * mul) >> shift); }
 };
 
 struct Batch {

@@ -772,23 +772,23 @@ __global__ void k_pad_rows(const int8_t* __restrict__ q, int rows, int k, int8_t
 // row tiles of activations and sc column tiles of weights in L2.  The map is a
 // bijection on [0, row_tiles * col_tiles) (the host picks gm dividing both
 // counts and sr dividing the region's row tiles).
-__device__ __forceinline__ void tile_of(const Proj& P, int i, int row_tiles, int& mt, int& nt) {
-  const int col_tiles = P.waves_n;
+// The divisions are multiply-shifts by host-computed Dividers (scalar ALU
+// only).
+__device__ __forceinline__ void tile_of(const Proj& P, int i, int& mt, int& nt) {
   if (P.xcd_gm == 0) {
-    mt = i / col_tiles;
-    nt = i - mt * col_tiles;
+    mt = P.d_cols.div((uint32_t)i);
+    nt = i - mt * P.waves_n;
     return;
   }
-  const int gm = P.xcd_gm, gn = 8 / gm;
-  const int rm = row_tiles / gm, rn = col_tiles / gn;  // region size in tiles
+  const int rm = P.xcd_rm, rn = P.xcd_rn;  // region size in tiles
   const int x = i & 7, j = i >> 3;
-  const int xa = x / gn, xb = x - xa * gn;
+  const int xa = x >> P.xcd_gn_shift, xb = x - (xa << P.xcd_gn_shift);
   const int sr = P.xcd_sr, sc = P.xcd_sc;
-  const int band = j / (sr * rn), t = j - band * (sr * rn);
-  const int chunk = t / (sr * sc), u = t - chunk * (sr * sc);
-  const int ur = u % sr;
+  const int band = P.d_band.div((uint32_t)j), t = j - band * (sr * rn);
+  const int chunk = P.d_chunk.div((uint32_t)t), u = t - chunk * (sr * sc);
+  const int uq = P.d_sr.div((uint32_t)u), ur = u - uq * sr;
   mt = xa * rm + band * sr + ur;
-  nt = xb * rn + chunk * sc + (u - ur) / sr;
+  nt = xb * rn + chunk * sc + uq;
 }
 
 // Direct global->LDS loads.  They are issued through inline assembly so the
@@ -983,7 +983,7 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   const int pidx = find_proj(b, blk);
   const Proj P = b.p[pidx];
   int mt, nt;
-  tile_of(P, blk - P.wave_begin, (P.m + BM - 1) / BM, mt, nt);
+  tile_of(P, blk - P.wave_begin, mt, nt);
   // A SwiGLU pair block covers BN/2 output columns: wave wn's column tile 0
   // is the gate projection's, tile 1 the up projection's, of the same 32
   // outputs (RT == 1, CT == 2 only).
