@@ -462,8 +462,9 @@ __device__ __forceinline__ float quant_scale_fma(float m) {
 // u = a + 128 is within 2^-17 of the exact sum, so when u lies more than 2^-14
 // from every half-integer, rint(u) = round(Q) + 128, an integer in [1, 255]
 // (|a| < 127.0001, no clamp needed), converted and packed by v_cvt_pk_u8_f32;
-// the XOR with 0x80 turns it into the two's complement byte.  A lane with an
-// element closer than that (about 1 in 8000 elements) divides all N exactly.
+// the XOR with 0x80 turns it into the two's complement byte.  A wave with an
+// element closer than that (about 1 in 8000 elements) divides all its
+// elements exactly.
 // FMA: u = v * rs + 128 rounded once instead of twice; u is then within 2^-16
 // + 2^-17 of Q + 128, inside the same margin.
 template <int N, bool FMA = false>
@@ -477,7 +478,11 @@ __device__ __forceinline__ void quant_pack(const float (&v)[N], float scale, uin
     r[i] = rintf(u);
     fm = fmaxf(fm, fabsf(u - r[i]));
   }
-  if (!(0.5f - fm > 0x1p-14f)) {
+  // Some element within 2^-14 of a rounding boundary: the exact quotients,
+  // decided per wave (they equal the shortcut wherever the margin holds), so
+  // the divisions run only in such waves instead of in every lane, selected.
+  if (__ballot(!(0.5f - fm > 0x1p-14f)) != 0) {
+    asm volatile("");  // keeps the divisions inside the branch
 #pragma unroll
     for (int i = 0; i < N; ++i) r[i] = fminf(fmaxf(roundf(v[i] / scale), -127.0f), 127.0f) + 128.0f;
   }
@@ -1273,17 +1278,16 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 #pragma unroll
           for (int i = 0; i < 16; ++i) e[i] = cb + i < P.n ? e[i] : 0.0f;
         }
-        float mx = 0.0f;
-        bool bad = false;
+        // absmax and the finite check from the magnitudes' bit patterns, as in
+        // k_quantize_loop (a NaN, only with the flag set, makes the scale NaN)
+        uint32_t mb = 0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          bad |= !isfinite(e[i]);
-          mx = fmaxf(mx, fabsf(e[i]));
-        }
-        mx = max_quad(mx);  // the group's 4 threads are lanes 4j .. 4j+3
-        const float scale = quant_scale(mx);
+        for (int i = 0; i < 16; ++i) mb = max(mb, __builtin_bit_cast(uint32_t, e[i]) & 0x7fffffffu);
+        const bool bad = mb >= 0x7f800000u;
+        const float mx = max_quad(__builtin_bit_cast(float, mb));  // the group's 4 threads are lanes 4j .. 4j+3
+        const float scale = quant_scale_fma(mx);
         uint32_t w4[4];
-        quant_pack<16>(e, scale, w4);
+        quant_pack<16, true>(e, scale, w4);
         if (row < P.m) {
           int8_t* qr = P.hq + (size_t)row * P.n + cb;
           if ((P.n & 15) == 0 && ((uintptr_t)P.hq & 15) == 0) {
