@@ -885,6 +885,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 #ifndef DQ8_WIDE_DEEP_MIXED
 #define DQ8_WIDE_DEEP_MIXED 1533
 #endif
+// Launches of at most DQ8_WIDE_DEEP4_BLOCKS blocks (two per CU) use a ring of
+// 4 groups (58 KB of LDS): down (2048 x 6144 -> 2048) 58.7 -> 56.2 us, the
+// 2048 x 2048 -> 2048 launches unchanged; a ring of 5 was slower (59.8 us).
+#ifndef DQ8_WIDE_DEEP4_BLOCKS
+#define DQ8_WIDE_DEEP4_BLOCKS 512
+#endif
 
 // ---------------------------------------------------------------------------
 // Wide projection kernel (M > 32), LDS-staged.  A block of WM x WN waves owns
@@ -2591,7 +2597,7 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
     // with few others wait on load latency between groups; a ring one group
     // deeper hides it.  That is the case for launches of at most three blocks
     // per CU (the 2048-row stack's 512- and 768-block launches: 2.4% off its
-    // step; a ring of STAGES + 2 at two blocks per CU measured slower), and for
+    // step; at two blocks per CU a ring of 4, see DQ8_WIDE_DEEP4_BLOCKS), and for
     // the trailing long-K blocks of a launch that mixes long and short K (a
     // layer's projection set over a few questions' rows: 22-28% faster for
     // 96-192 rows, 1-3% at 384).  Above three blocks per CU the deeper ring's
@@ -2618,6 +2624,7 @@ hipError_t launch_linear(const Batch& b, int kind, bool dots, hipStream_t s) {
       return hipGetLastError();
     }
     if (dots) DQ8_WIDE(S0, S0, X, true, false);
+    else if (b.total_waves <= DQ8_WIDE_DEEP4_BLOCKS) lora ? DQ8_WIDE(4, 4, X, false, true) : DQ8_WIDE(4, 4, X, false, false);
 #if DQ8_WIDE_SPLIT == 0
     else if (lora) deep ? DQ8_WIDE(S1, S1, X, false, true) : DQ8_WIDE(S0, S0, X, false, true);
     else deep ? DQ8_WIDE(S1, S1, X, false, false) : DQ8_WIDE(S0, S0, X, false, false);
