@@ -2265,16 +2265,33 @@ __device__ __forceinline__ void lora_mid_small(const float* __restrict__ x, int 
   lds_barrier();
   if (tid >= NT) return;  // wave-uniform: NT is a multiple of 64
   const int pr = tid >> 3, i = tid & 7, r = pr / J, j = pr - r * J;
-  const float* xs = lds + r * RS;
-  const float* as = lds + (R + j) * RS;
+  // Both row bases as opaque LDS addresses: the compiler would otherwise fold
+  // the constant R * RS * 4 (over 64 KB) into every read's offset and, since
+  // the offset field stops at 64 KB, rebuild each read's address on the VALU.
+  typedef __attribute__((address_space(3))) const float* lds_row;
+  lds_row xs = (lds_row)(lds + r * RS);
+  lds_row as = (lds_row)(lds + (R + j) * RS);
+  // this lane's elements i, i + 8, ...: one address step per CU chunks, the
+  // chunks within it as immediate offsets; all CU chunks' operands are read
+  // before the first is summed, so one LDS latency per CU chunks is exposed
+  // (the chain's adds hide the rest)
+  constexpr int CU = 32;
+  lds_row xp = xs + i, ap = as + i;
+  asm volatile("" : "+v"(xp), "+v"(ap));
   const int chunks = k >> 3;
   float acc = 0.0f;
   int c = 0;
-  for (; c + 8 <= chunks; c += 8) {
+  for (; c + CU <= chunks; c += CU, xp += 8 * CU, ap += 8 * CU) {
+    float xv[CU], av[CU];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc = acc + xs[8 * (c + u) + i] * as[8 * (c + u) + i];
+    for (int u = 0; u < CU; ++u) {
+      xv[u] = xp[8 * u];
+      av[u] = ap[8 * u];
+    }
+#pragma unroll
+    for (int u = 0; u < CU; ++u) acc = acc + xv[u] * av[u];
   }
-  for (; c < chunks; ++c) acc = acc + xs[8 * c + i] * as[8 * c + i];
+  for (; c < chunks; ++c, xp += 8, ap += 8) acc = acc + xp[0] * ap[0];
   float sum = -0.0f;
 #pragma unroll
   for (int ii = 0; ii < 8; ++ii) sum = sum + __shfl(acc, (lane & ~7) + ii);
