@@ -256,10 +256,22 @@ __device__ __forceinline__ void store_tile_full(const Proj& P, const int (&ur)[E
   }
 }
 
+// The projection of a launch's block: the last one whose first block is at
+// most `wave`.  UNROLL: over the batch's fixed capacity, so the kernel
+// argument loads go out together (one latency) rather than one per item: the
+// skinny kernel's grouped launches of 9 projections start 2 us sooner (the
+// wide kernel's launches hold 1 to 3 and measured slower so).
+template <bool UNROLL = false>
 __device__ __forceinline__ int find_proj(const Batch& b, int wave) {
   int pi = 0;
-  for (int i = 1; i < b.count; ++i)
-    if (wave >= b.p[i].wave_begin) pi = i;
+  if constexpr (UNROLL) {
+#pragma unroll
+    for (int i = 1; i < kMaxBatch; ++i)
+      if (i < b.count && wave >= b.p[i].wave_begin) pi = i;
+  } else {
+    for (int i = 1; i < b.count; ++i)
+      if (wave >= b.p[i].wave_begin) pi = i;
+  }
   return pi;
 }
 
@@ -1932,10 +1944,11 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
 template <int RT, int CT, int CTL, int DBS, int DBL, bool DOTS, bool LORA>
 __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[skinny_lds_bytes(RT, CTL)];
+  const int pidx = find_proj<true>(b, blockIdx.x);
   if (b.unless && *b.unless) return;  // non-finite inputs: the FP32 kernel runs instead
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const Proj& P = b.p[find_proj(b, blockIdx.x)];
+  const Proj& P = b.p[pidx];
   const int local = blockIdx.x - P.wave_begin;
   if (P.nseg == 1) {
     static_assert(CT == 2, "short-K waves take at most two 16-column units");
