@@ -382,7 +382,10 @@ void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips, long lau
       // short K: 16-column units dealt to blocks, units_per_block at a time
       p.waves_n = (p.n + 15) / 16;
       p.units = units_per_block(launch_units, launch_has_long);
-      b.total_waves += (p.waves_n + p.units - 1) / p.units;
+      const int blocks = (p.waves_n + p.units - 1) / p.units;
+      p.deal_q = p.waves_n / blocks;
+      p.deal_r = p.waves_n % blocks;
+      b.total_waves += blocks;
     } else {
       // long K: one 16-row tile of a strip per block (kind 2: two per strip)
       p.waves_n = (p.n + dq8::skinny_cols(p.nseg) - 1) / dq8::skinny_cols(p.nseg);

@@ -64,6 +64,8 @@ struct Proj {
   int waves_n;        // column strips (wide: one block tile wide; skinny long K: 16 columns wide;
                       // skinny short K: 16-column units, dealt to blocks `units` at a time)
   int units;          // skinny short K: at most this many 16-column units per block (2..8)
+  int deal_q, deal_r; // skinny short K: the waves_n units over B = ceil(waves_n / units) blocks,
+                      // deal_q = waves_n / B each and one more for the first deal_r = waves_n % B
   int xcd_gm;         // wide: row bands of the per-XCD tile regions (1, 2, 4, 8), 0 = row-major order
   int xcd_sr, xcd_sc; // wide: a region is walked in chunks of xcd_sr row tiles x xcd_sc column tiles
   // wide: the tile walk's divisors, set with the fields above: region size in

@@ -1959,13 +1959,12 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
       u0 = 2 * (4 * local + wid);
       cnt = u0 < H ? 2 : 0;
     } else {
-      // The units are dealt to B = ceil(H / units) blocks, floor(b*H/B) ..
-      // floor((b+1)*H/B) to block b (at most 7), so blocks carry equal byte
-      // counts to within one unit, and a block's c units to its waves as
-      // evenly as they go (w*c/4 .. (w+1)*c/4): as many waves stream as the
-      // block has units, up to 4, and none takes more than two.
-      const long B = (H + P.units - 1) / P.units;
-      const int h0 = (int)((long)local * H / B), c = (int)((long)(local + 1) * H / B) - h0;
+      // The units are dealt to B = ceil(H / units) blocks, deal_q to each and
+      // one more to the first deal_r (at most 7; the host divides), so blocks
+      // carry equal byte counts to within one unit, and a block's c units to
+      // its waves as evenly as they go (w*c/4 .. (w+1)*c/4): as many waves
+      // stream as the block has units, up to 4, and none takes more than two.
+      const int h0 = local * P.deal_q + min(local, P.deal_r), c = P.deal_q + (local < P.deal_r ? 1 : 0);
       u0 = h0 + wid * c / 4;
       cnt = h0 + (wid + 1) * c / 4 - u0;
     }
@@ -1985,7 +1984,8 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
     const int run = local >> 4, in = local & 15;
     const int left = P.waves_n - 8 * run;  // strips from this run on
     const int r = left >= 8 ? 8 : left;
-    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, 8 * run + in % r, wid, lane, lds, 16 * (in / r));
+    const int t = r == 8 ? in >> 3 : in / r;  // the row tile (a division only in the last run)
+    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, 8 * run + in - t * r, wid, lane, lds, 16 * t);
   }
 }
 // LoRA middle product (weights.rs:480, 495): mid[r][j] = dot_scores(x_r, a_j)
