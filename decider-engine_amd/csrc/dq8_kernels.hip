@@ -1948,7 +1948,7 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   if (b.unless && *b.unless) return;  // non-finite inputs: the FP32 kernel runs instead
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const Proj& P = b.p[pidx];
+  const Proj P = b.p[pidx];  // by value: its fields load in one batch
   const int local = blockIdx.x - P.wave_begin;
   if (P.nseg == 1) {
     static_assert(CT == 2, "short-K waves take at most two 16-column units");
