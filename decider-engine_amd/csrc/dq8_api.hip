@@ -356,6 +356,7 @@ bool small_call(const Item* items, size_t count, W weights_of) {
 // wave/block, column strips, XCD split and the launch's running total.
 void place_proj(dq8::Proj& p, int kind, dq8::Batch& b, bool few_strips, long launch_units, bool launch_has_long) {
   p.wave_begin = b.total_waves;
+  b.wave_begin[&p - b.p] = p.wave_begin;
   p.xcd_gm = 0;
   p.nseg = 1;
   if (kind == 0) {

@@ -97,6 +97,7 @@ struct Proj {
 
 struct Batch {
   Proj p[kMaxBatch];
+  int wave_begin[kMaxBatch];  // p[i].wave_begin, contiguous: one scalar load finds a block's projection
   int count;
   int total_waves;  // blocks of the launch
   int any_lora;     // some projection has a LoRA adapter (selects the kernels with the LoRA epilogue)

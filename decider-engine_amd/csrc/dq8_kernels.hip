@@ -257,17 +257,19 @@ __device__ __forceinline__ void store_tile_full(const Proj& P, const int (&ur)[E
 }
 
 // The projection of a launch's block: the last one whose first block is at
-// most `wave`.  UNROLL: over the batch's fixed capacity, so the kernel
-// argument loads go out together (one latency) rather than one per item: the
+// most `wave`.  UNROLL: over the batch's fixed capacity and the contiguous
+// copy of the first blocks, so the kernel argument loads are one or two
+// instructions with one latency rather than one round trip per item: the
 // skinny kernel's grouped launches of 9 projections start 2 us sooner (the
-// wide kernel's launches hold 1 to 3 and measured slower so).
+// wide kernel's launches hold 1 to 3 and measured slower with the per-item
+// form of this).
 template <bool UNROLL = false>
 __device__ __forceinline__ int find_proj(const Batch& b, int wave) {
   int pi = 0;
   if constexpr (UNROLL) {
 #pragma unroll
     for (int i = 1; i < kMaxBatch; ++i)
-      if (i < b.count && wave >= b.p[i].wave_begin) pi = i;
+      if (i < b.count && wave >= b.wave_begin[i]) pi = i;
   } else {
     for (int i = 1; i < b.count; ++i)
       if (wave >= b.p[i].wave_begin) pi = i;
@@ -1699,7 +1701,8 @@ __device__ __forceinline__ void skinny_group(const Proj& P, int c0, int lane, bo
 // groups, 2 groups per step.  The block's 4 waves first load its activation
 // together; a wave with no columns (live false) only helps with that.
 template <int RT, int CT, int DB, bool DOTS, bool LORA>
-__device__ __forceinline__ void skinny_short(const Proj& P, int c0, bool live, int wid, int lane, uint8_t* lds) {
+__device__ __forceinline__ void skinny_short(const Proj& P, int c0, bool live, int wid, int lane, uint8_t* lds,
+                                             const uint32_t* unless) {
   constexpr int ROWS = 16 * RT;
   constexpr int STEP_A = RT * 2 * kFragBytes;  // activation bytes of one step (8-row units)
   constexpr int OPS = 2 * CT * (DOTS ? 1 : 2);  // ring loads per step
@@ -1749,7 +1752,11 @@ __device__ __forceinline__ void skinny_short(const Proj& P, int c0, bool live, i
     }
     if constexpr (!DOTS) issue_x_chunk<ROWS, 8>(P, 0, wid, xl);
   }
+  // the non-finite flag is read while the first loads are in flight; the
+  // whole block leaves on it (after they land: they write this block's LDS)
+  const bool skip = unless != nullptr && *unless != 0;
   wait_vmcnt<0>();
+  if (skip) return;
   lds_barrier();
   if (!live) return;  // no later barrier in this path
 
@@ -1814,7 +1821,8 @@ __device__ __forceinline__ void skinny_short(const Proj& P, int c0, bool live, i
 // Long K (G > 32): one strip per block (TPB = 4/NSEG = 1), its 16*RT rows from row
 // r0, NSEG waves, one group per wave and step.
 template <int RT, int CT, int DB, int NSEG, bool DOTS, bool LORA>
-__device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, int lane, uint8_t* lds, int r0) {
+__device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, int lane, uint8_t* lds, int r0,
+                                            const uint32_t* unless) {
   constexpr int ROWS = 16 * RT, NT = RT * CT, TPB = 4 / NSEG;
   constexpr int XP = 2 * NSEG;                 // x pieces per row of a chunk of 8 steps (8*NSEG groups)
   constexpr int XBYTES = ROWS * XP * 16;
@@ -1884,6 +1892,12 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
     issue(aq[d], bq[d], wq[d], min(d, steps - 1));
     __builtin_amdgcn_sched_barrier(0);
   }
+  // the non-finite flag, read while the first loads are in flight (the block
+  // leaves after they land: the x chunk writes this block's LDS)
+  if (unless != nullptr && *unless != 0) {
+    wait_vmcnt<0>();
+    return;
+  }
   // Step j from ring slot d (a constant after unrolling); as in the short-K
   // loop, every slot is consumed on every path and the ring loop has no early
   // exit.  Groups past G (the last step) are computed on clamped copies; their
@@ -1944,8 +1958,9 @@ __device__ __forceinline__ void skinny_long(const Proj& P, int local, int wid, i
 template <int RT, int CT, int CTL, int DBS, int DBL, bool DOTS, bool LORA>
 __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[skinny_lds_bytes(RT, CTL)];
+  // non-finite inputs (*b.unless != 0): the FP32 kernel runs instead; each
+  // path checks the flag once its first loads are out
   const int pidx = find_proj<true>(b, blockIdx.x);
-  if (b.unless && *b.unless) return;  // non-finite inputs: the FP32 kernel runs instead
   const int lane = threadIdx.x & 63;
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const Proj P = b.p[pidx];  // by value: its fields load in one batch
@@ -1969,11 +1984,11 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
       cnt = h0 + (wid + 1) * c / 4 - u0;
     }
     if (cnt == 2)
-      skinny_short<RT, 2, DBS, DOTS, LORA>(P, 16 * u0, true, wid, lane, lds);
+      skinny_short<RT, 2, DBS, DOTS, LORA>(P, 16 * u0, true, wid, lane, lds, b.unless);
     else
-      skinny_short<RT, 1, DBS, DOTS, LORA>(P, 16 * u0, cnt == 1, wid, lane, lds);
+      skinny_short<RT, 1, DBS, DOTS, LORA>(P, 16 * u0, cnt == 1, wid, lane, lds, b.unless);
   } else if (RT == 1) {
-    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, local, wid, lane, lds, 0);
+    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, local, wid, lane, lds, 0, b.unless);
   } else {
     // One 16-row tile per block: 17-32 rows take two blocks per strip.  The
     // two blocks of a strip are 8 apart (blocks are dealt to the 8 XCDs in
@@ -1985,7 +2000,7 @@ __global__ __launch_bounds__(256) void k_linear_skinny(Batch b) {
     const int left = P.waves_n - 8 * run;  // strips from this run on
     const int r = left >= 8 ? 8 : left;
     const int t = r == 8 ? in >> 3 : in / r;  // the row tile (a division only in the last run)
-    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, 8 * run + in - t * r, wid, lane, lds, 16 * t);
+    skinny_long<1, CTL, DBL, 4, DOTS, LORA>(P, 8 * run + in - t * r, wid, lane, lds, 16 * t, b.unless);
   }
 }
 // LoRA middle product (weights.rs:480, 495): mid[r][j] = dot_scores(x_r, a_j)
