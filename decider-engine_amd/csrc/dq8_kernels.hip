@@ -994,7 +994,8 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   };
   __shared__ __attribute__((aligned(16))) Ring ring;
   __shared__ __attribute__((aligned(16))) XChunk xc[DOTS ? 1 : 2];
-  if (b.unless && *b.unless) return;  // non-finite inputs: the FP32 kernel runs instead
+  // Non-finite inputs (*b.unless != 0): the FP32 kernel runs instead.  The
+  // flag is read once a tile's first loads are out.
 
   // One tile (block index blk of the launch's tile list).
   auto run_tile = [&](const int blk) {
@@ -1005,7 +1006,7 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   asm volatile("" : "+v"(lane));
 #endif
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-  const int pidx = find_proj(b, blk);
+  const int pidx = find_proj<true>(b, blk);
   const Proj P = b.p[pidx];
   int mt, nt;
   tile_of(P, blk - P.wave_begin, mt, nt);
@@ -1126,6 +1127,10 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
     if (i < SA - 1) issue_a(ring.a[i], i);
     issue_b(ring.b[i], i);
     __builtin_amdgcn_sched_barrier(0);
+  }
+  if (b.unless && *b.unless) {  // uniform: the block leaves once its loads into LDS have landed
+    wait_vmcnt<0>();
+    return;
   }
   for (int g0 = 0; g0 < G; g0 += PERIOD) {
 #pragma unroll
