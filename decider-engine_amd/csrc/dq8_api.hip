@@ -1095,6 +1095,7 @@ dq8_status dq8_lora_mid_batch(dq8_ctx* ctx, const dq8_lora_mid_item* items, size
       b[t].count = 0;
       blocks[t] = 0;
     }
+    b[t].block_begin[b[t].count] = (int)blocks[t];
     b[t].it[b[t].count++] = {it.x, it.a, it.mid, m, k, rank, (int)blocks[t]};
     blocks[t] += nb;
   }

@@ -117,6 +117,7 @@ struct MidItem {
 };
 struct MidBatch {
   MidItem it[kMaxMids];
+  int block_begin[kMaxMids];  // it[i].block_begin, contiguous: two scalar loads find a block's item
   int count;
 };
 

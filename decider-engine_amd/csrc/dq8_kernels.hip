@@ -2254,15 +2254,21 @@ __global__ __launch_bounds__(256) void k_lora_mid_dma(const float* __restrict__ 
   __shared__ __attribute__((aligned(16))) MidTile lds;
   lora_mid_tiled(x, m, k, a, rank, mid, (int)blockIdx.x, lds);
 }
-// Several tiled middle products in one launch (block -> item as in
-// k_lora_mid_small_batch).
+// The item of block b of a grouped middle-product launch: the last one whose
+// first block is <= b (block_begin ascends).  Unrolled over the table of first
+// blocks, so its loads go out together rather than one round trip per item.
+__device__ __forceinline__ int find_mid(const MidBatch& bt, int b) {
+  int it = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxMids; ++i)
+    if (i < bt.count && b >= bt.block_begin[i]) it = i;
+  return it;
+}
+// Several tiled middle products in one launch.
 __global__ __launch_bounds__(256) void k_lora_mid_dma_batch(MidBatch bt) {
   __shared__ __attribute__((aligned(16))) MidTile lds;
   const int b = (int)blockIdx.x;
-  int it = 0;
-  for (int i = 1; i < bt.count; ++i)
-    if (b >= bt.it[i].block_begin) it = i;
-  const MidItem& I = bt.it[it];
+  const MidItem I = bt.it[find_mid(bt, b)];
   lora_mid_tiled(I.x, I.m, I.k, I.a, I.rank, I.mid, b - I.block_begin, lds);
 }
 
@@ -2339,15 +2345,11 @@ __global__ __launch_bounds__(256) void k_lora_mid_small(const float* __restrict_
   __shared__ __attribute__((aligned(16))) float lds[(kSmallR + kSmallJ) * kSmallRS];
   lora_mid_small<kSmallR, kSmallJ, kSmallKR>(x, m, k, a, rank, mid, (int)blockIdx.x, lds);
 }
-// Several middle products in one launch: block b belongs to the last item whose
-// first block is <= b (block_begin ascends).
+// Several middle products in one launch (block -> item by find_mid).
 __global__ __launch_bounds__(256) void k_lora_mid_small_batch(MidBatch bt) {
   __shared__ __attribute__((aligned(16))) float lds[(kSmallR + kSmallJ) * kSmallRS];
   const int b = (int)blockIdx.x;
-  int it = 0;
-  for (int i = 1; i < bt.count; ++i)
-    if (b >= bt.it[i].block_begin) it = i;
-  const MidItem& I = bt.it[it];
+  const MidItem I = bt.it[find_mid(bt, b)];
   lora_mid_small<kSmallR, kSmallJ, kSmallKR>(I.x, I.m, I.k, I.a, I.rank, I.mid, b - I.block_begin, lds);
 }
 
