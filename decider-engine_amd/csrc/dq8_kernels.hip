@@ -1702,6 +1702,15 @@ __device__ __forceinline__ void skinny_group(const Proj& P, int c0, int lane, bo
     }
 }
 
+// 1: the short-K weight loads are non-temporal: each weight byte is read once,
+// and the stream no longer displaces the activations and the long-K weights
+// that the other blocks re-read from L2 (24-row layer set: 18.5 -> 17.2 us per
+// question launch).  Non-temporal w-scale loads measured no better, and
+// non-temporal long-K weight loads slower (both row-tile blocks of a strip
+// read them).
+#ifndef DQ8_SKINNY_NT_SHORT
+#define DQ8_SKINNY_NT_SHORT 1
+#endif
 // Short K (G <= 32): one wave streams the 16*CT columns from c0 over all
 // groups, 2 groups per step.  The block's 4 waves first load its activation
 // together; a wave with no columns (live false) only helps with that.
@@ -1733,7 +1742,11 @@ __device__ __forceinline__ void skinny_short(const Proj& P, int c0, bool live, i
       const int g = min(2 * j + gi, G - 1);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
+#if DQ8_SKINNY_NT_SHORT
+        bs[gi][ct] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(pb[ct] + (size_t)g * 2 * kFragBytes));
+#else
         bs[gi][ct] = load16(pb[ct] + (size_t)g * 2 * kFragBytes);
+#endif
         if constexpr (!DOTS) ws[gi][ct] = pw[ct][(size_t)g * P.np];
       }
     }
