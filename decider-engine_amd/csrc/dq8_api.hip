@@ -168,8 +168,18 @@ dq8_status ensure_work(dq8_ctx* ctx, size_t bytes, hipStream_t s) {
   return ensure_buffer(ctx, ctx->work, ctx->work_bytes, bytes, s);
 }
 
+// Weight shapes a handle can hold: n and k from 1 to 2^30 with n*k <= 2^40,
+// and the bounds under which the projection kernels form each group's operand
+// offsets in 32 bits: k <= 2^26 (group offsets below 2^31) and a w-scale table
+// (np rows of G + 1 floats, the last row zero) under 4 GiB.
+bool weight_shape_ok(size_t n, size_t k) {
+  if (n == 0 || k == 0 || n > (1u << 30) || k > (1u << 26) || n * k > ((size_t)1 << 40)) return false;
+  const size_t np = (n + dq8::kColPad - 1) / dq8::kColPad * dq8::kColPad;
+  return np * (groups_of(k) + 1) * sizeof(float) < ((size_t)1 << 32);
+}
+
 dq8_status make_weights(dq8_ctx* ctx, size_t n, size_t k, dq8_weights** out) {
-  if (n == 0 || k == 0 || n > (1u << 30) || k > (1u << 30) || n * k > ((size_t)1 << 40)) return DQ8_ERR_SHAPE;
+  if (!weight_shape_ok(n, k)) return DQ8_ERR_SHAPE;
   dq8_weights* h = new (std::nothrow) dq8_weights();
   if (!h) return DQ8_ERR_NOMEM;
   h->w.device = ctx->device;
@@ -760,7 +770,7 @@ dq8_status stage_to_device(dq8_ctx* ctx, uint8_t* dst, size_t bytes, hipStream_t
 }
 
 size_t raw_element_bytes(int dtype) { return dtype == dq8::kDtypeF32 ? 4 : 2; }
-bool raw_shape_ok(size_t n, size_t k) { return n && k && n <= (1u << 30) && k <= (1u << 30) && n * k <= ((size_t)1 << 40); }
+bool raw_shape_ok(size_t n, size_t k) { return weight_shape_ok(n, k); }
 
 // Data::quantize of n*k stored elements at device address raw (weights.rs:98-146),
 // then the repack into a new handle.  Non-finite elements: DQ8_ERR_NONFINITE,

@@ -1023,10 +1023,10 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
 
   // 16-byte loads: slot k of this wave is load i = k*NW + wid (A slab i, or B
   // fragment i - AS), landing at frag[i].  Address = uniform base + group *
-  // stride (scalar) + a fixed lane offset.
+  // stride (scalar: 64 bytes for an A slab, 2 KB for a B fragment pair) + a
+  // fixed lane offset.
   const uint8_t* sbase[L16];
   uint32_t loff[L16];
-  int stride[L16];
 #pragma unroll
   for (int k = 0; k < L16; ++k) {
     const int i = k * NW + wid;
@@ -1036,19 +1036,16 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
       const int row = min(m0 + 16 * i + rr, P.m - 1);
       sbase[k] = reinterpret_cast<const uint8_t*>(P.q) + (size_t)r0 * P.ldq;
       loff[k] = (uint32_t)((row - r0) * P.ldq + 16 * ((lane & 3) ^ swz(rr)));
-      stride[k] = kGroup;
     } else if (pair) {
       // fragment fb: column tile ct = fb/2 of the block is tile ct%2 (gate or
       // up) of wave ct/2, output columns n0 + 32*(ct/2) ..
       const int fb = i - AS, ct = fb >> 1;
       sbase[k] = ((ct & 1) ? P.wt2 : P.wt) + ((size_t)(n0 / 32 + (ct >> 1)) * G * 2 + (fb & 1)) * kFragBytes;
       loff[k] = (uint32_t)lane * 16;
-      stride[k] = 2 * kFragBytes;
     } else {
       const int fb = i - AS;
       sbase[k] = P.wt + ((size_t)(n0 / 32 + (fb >> 1)) * G * 2 + (fb & 1)) * kFragBytes;
       loff[k] = (uint32_t)lane * 16;
-      stride[k] = 2 * kFragBytes;
     }
   }
   // w scales: wave w < WSD loads columns 64w .. 64w+63; the others repeat wave
@@ -1057,20 +1054,24 @@ __global__ __launch_bounds__(64 * WM * WN) DQ8_WIDE_ATTR void k_linear_wide(Batc
   // wave 1 the up scales, to ws[0..63] and ws[64..127].)
   const int ww = WSD > 0 ? wid % (WSD > 0 ? WSD : 1) : 0;
   const float* wsbase = pair ? (ww ? P.wst2 : P.wst) + n0 : P.wst + n0 + 64 * ww;
+  const uint32_t wsrow = 4u * (uint32_t)P.np;  // bytes per w-scale row
   // x-scale pieces: load d = k*NW + wid of a chunk covers rows RPD*d .. RPD*d+RPD-1;
   // lane l fetches row l/PPR, piece (l%PPR) ^ (row%PPR).
 
+  // A group's offsets are formed in 32 bits (one scalar add with carry per
+  // load): weight handles keep k <= 2^26 and their w-scale table under 4 GiB.
   auto issue_a = [&](AStage& S, int g) {
-    const int gc = min(g, G - 1);
+    const uint32_t gc = (uint32_t)min(g, G - 1);
 #pragma unroll
-    for (int k = 0; k < KA; ++k) dma16s(sbase[k] + (size_t)gc * stride[k], loff[k], &S.frag[k * NW + wid][0]);
+    for (int k = 0; k < KA; ++k) dma16s(sbase[k] + gc * (uint32_t)kGroup, loff[k], &S.frag[k * NW + wid][0]);
   };
   auto issue_b = [&](BStage& S, int g) {
-    const int gc = min(g, G - 1);
+    const uint32_t gc = (uint32_t)min(g, G - 1);
 #pragma unroll
     for (int k = KA; k < L16; ++k)
-      dma16s(sbase[k] + (size_t)gc * stride[k], loff[k], &S.frag[k * NW + wid - AS][0]);
-    if constexpr (!DOTS) dma4s(wsbase + (size_t)min(g, G) * P.np, (uint32_t)lane * 4, &S.ws[64 * ww]);
+      dma16s(sbase[k] + gc * (uint32_t)(2 * kFragBytes), loff[k], &S.frag[k * NW + wid - AS][0]);
+    if constexpr (!DOTS)
+      dma4s(reinterpret_cast<const char*>(wsbase) + (uint32_t)min(g, G) * wsrow, (uint32_t)lane * 4, &S.ws[64 * ww]);
   };
   auto issue_x = [&](int c) {  // once per XCH groups: addresses are recomputed here, not kept live
     int ln;  // lane id, read here so that nothing derived from it stays live across the loop

@@ -5,6 +5,8 @@ identical; fp32 outputs of Write/Add/SwiGlu must be identical (the stated
 tolerance is max relative error 1e-6; the kernels meet it exactly).  SwiGlu's
 silu runs glibc's expf algorithm on the device; the oracle calls libm expf.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -165,6 +167,19 @@ def test_linear_rejects_grids_out_of_range(ctx):
     fake = 256
     for m in ((1 << 28) + 1, (1 << 30) + 1):
         assert lib.dq8_linear(ctx.handle, h.handle, fake, fake, m, None, fake, 0, 0, None) == dq8.ERR_SHAPE
+    torch.cuda.synchronize()
+
+
+def test_weights_reject_shapes_beyond_the_offset_bounds(ctx):
+    # k > 2^26, or a scale table of 4 GiB or more: DQ8_ERR_SHAPE from every
+    # weight constructor before anything is read (stand-in pointers)
+    lib = dq8.lib()
+    fake = 256
+    for n, k in ((1, (1 << 26) + 64), (1 << 26, 1 << 10)):
+        out = ctypes.c_void_p()
+        assert lib.dq8_weights_from_f32(ctx.handle, fake, n, k, None, ctypes.byref(out)) == dq8.ERR_SHAPE
+        assert lib.dq8_weights_from_quantized(ctx.handle, fake, fake, n, k, None, ctypes.byref(out)) == dq8.ERR_SHAPE
+        assert out.value is None
     torch.cuda.synchronize()
 
 
