@@ -276,6 +276,29 @@ def test_linear_add_epilogue_bit_exact(ctx, m, k, n):
     assert bits_equal(host(out), dq8o.linear(x, wv, ws, result=prev, epilogue=1, threads=4))
 
 
+@pytest.mark.parametrize("m,k,n,ep", [(130, 16384, 200, dq8.WRITE), (300, 12288, 130, dq8.ADD),
+                                      (24, 16384, 100, dq8.WRITE), (20, 32768, 48, dq8.ADD), (9, 20480, 40, dq8.WRITE)])
+def test_linear_long_k_bit_exact(ctx, m, k, n, ep):
+    # K far beyond the model's 6144 (192 to 512 groups): the wide kernel's operand
+    # rings and x-scale chunk buffers, and the skinny long-K ring and in-order
+    # hand-off, wrap many times; the group offsets reach the largest values tested
+    rng = np.random.default_rng(m + k + 7 * n)
+    x = make_x(rng, m, k, "student")
+    w = make_w(rng, n, k)
+    wv, ws = dq8o.quantize_weights(w)
+    h = ctx.weights_from_quantized(dev(wv), dev(ws))
+    q, s = ctx.quantize(dev(x))
+    if ep == dq8.ADD:
+        prev = rng.standard_normal((m, n)).astype(np.float32)
+        out = dev(prev)
+        ctx.linear(h, q, s, out=out, epilogue=dq8.ADD)
+        want = dq8o.linear(x, wv, ws, result=prev, epilogue=1, threads=4)
+    else:
+        out = ctx.linear(h, q, s)
+        want = dq8o.linear(x, wv, ws, threads=4)
+    assert bits_equal(host(out), want)
+
+
 @pytest.mark.parametrize("m,k,n", [(3, 131, 31), (24, 2048, 64), (67, 192, 65), (50, 2048, 70)])
 def test_linear_swiglu_epilogue(ctx, m, k, n):
     rng = np.random.default_rng(5 * m + k + n)
