@@ -168,10 +168,10 @@ dq8_status ensure_work(dq8_ctx* ctx, size_t bytes, hipStream_t s) {
   return ensure_buffer(ctx, ctx->work, ctx->work_bytes, bytes, s);
 }
 
-// Weight shapes a handle can hold: n and k from 1 to 2^30 with n*k <= 2^40,
-// and the bounds under which the projection kernels form each group's operand
-// offsets in 32 bits: k <= 2^26 (group offsets below 2^31) and a w-scale table
-// (np rows of G + 1 floats, the last row zero) under 4 GiB.
+// Weight shapes a handle can hold: n from 1 to 2^30 and k from 1 to 2^26 with
+// n*k <= 2^40.  The bounds on k and on the w-scale table (G + 1 rows of np
+// floats, the last row zero; under 4 GiB) let the projection kernels form each
+// group's operand offsets in 32 bits (group offsets below 2^31).
 bool weight_shape_ok(size_t n, size_t k) {
   if (n == 0 || k == 0 || n > (1u << 30) || k > (1u << 26) || n * k > ((size_t)1 << 40)) return false;
   const size_t np = (n + dq8::kColPad - 1) / dq8::kColPad * dq8::kColPad;

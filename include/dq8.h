@@ -15,9 +15,10 @@
  *     Shape errors return DQ8_ERR_SHAPE where the crate panics (assert_eq!).
  *     A projection call also returns it for m > 2^30 rows or more than 2^39
  *     outputs (m * n) in one item, which keeps every launch's grid in range.
- *     Weight handles take n and k from 1 to 2^30 with n * k <= 2^40, k <= 2^26,
- *     and a scale table of ceil(n/256)*256 x (ceil(k/64) + 1) floats under
- *     4 GiB (about 64 GiB of int8 weights); larger shapes return it too.
+ *     Weight handles take n from 1 to 2^30 and k from 1 to 2^26 with
+ *     n * k <= 2^40 and a scale table of ceil(n/256)*256 x (ceil(k/64) + 1)
+ *     floats under 4 GiB (about 64 GiB of int8 weights); larger shapes return
+ *     it too.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).
  *     Weight handles are immutable after creation, so calls on different
  *     streams may share them.  One context must not be used by two host
