@@ -706,7 +706,7 @@ def test_lora_mid_unaligned_buffers(ctx, m, k, rank):
 # with full chunks of 8, tails, both, and rank 0.
 LORA_SHAPES = [(1, 64, 4, 3), (5, 131, 31, 13), (24, 2048, 96, 16), (17, 6144, 40, 8), (32, 256, 70, 1),
                (67, 131, 31, 13), (130, 2048, 100, 16), (64, 192, 65, 24), (19, 128, 9, 0), (48, 2048, 96, 16),
-               (37, 6144, 40, 8)]
+               (37, 6144, 40, 8), (130, 16384, 100, 16), (24, 12288, 64, 16), (300, 20480, 40, 8)]
 
 
 def _lora_case(rng, m, k, n, rank):
